@@ -1,0 +1,38 @@
+"""MI355X (gfx950) implementation of collab_infer's per-device attention hot path.
+
+Import with ``importlib.import_module("collaborative-edge-system_amd")``.  Modules:
+
+* :mod:`.attention` - ``attention_with_lse``, ``attention``, ``merge_attention``,
+  ``merge_attention_list`` and helpers (collab_infer/parallel/attention.py)
+* :mod:`.sequence_parallel` - one rank's ring / Ulysses / distributed-KV share on one GPU
+  (collab_infer/parallel/sequence_parallel.py)
+* :mod:`.layers` - RMSNorm, rotary, SiLU-gate (collab_infer/models/llama.py)
+* :mod:`.partition` - splits and sequence layouts (collab_infer/parallel/partition.py)
+* :mod:`.workloads` - seeded inputs of the five measured workloads
+"""
+
+from . import _native, attention, layers, partition, sequence_parallel, workloads  # noqa: F401
+from .attention import (  # noqa: F401
+    MASK_CHUNK_ELEMENTS,
+    accumulation_dtype,
+    attention as attention_fn,
+    attention_with_lse,
+    attention_with_lse_into,
+    expand_kv,
+    fully_masked,
+    gqa_group,
+    merge_attention,
+    merge_attention_list,
+    visibility_mask,
+)
+from .layers import RMSNorm, RotaryEmbedding, apply_rotary, rmsnorm, rmsnorm_rope, silu_mul  # noqa: F401
+from .partition import HeadShard, SequenceLayout, partition_heads, split_sizes  # noqa: F401
+from .sequence_parallel import (  # noqa: F401
+    LocalGroup,
+    distributed_kv_attention,
+    partitioned_attention,
+    ring_attention,
+    ulysses_attention,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,205 @@
+"""ctypes binding of the C ABI declared in ``include/collab_edge_attn.h``.
+
+The shared library is built in-tree (``build.py``) and loaded from ``_lib/``.  There is no
+fallback: when the library is missing or a tensor is not on a ROCm device, the calls raise.
+Status codes map onto the exception types the reference raises for the same conditions
+(``ValueError`` for inconsistent shapes / maps, ``NotImplementedError`` for unsupported
+requests, ``RuntimeError`` for launch failures).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import threading
+from pathlib import Path
+from typing import List, Optional, Sequence
+
+import torch
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "_lib" / "libcollab_edge_attn.so"
+HEADER_PATH = PKG_DIR.parent / "include" / "collab_edge_attn.h"
+
+MAX_DIMS = 4
+MAX_PARTS = 16
+
+DTYPE_CODES = {
+    torch.float32: 0,
+    torch.bfloat16: 1,
+    torch.float16: 2,
+    torch.float64: 3,
+    torch.int64: 4,
+}
+
+OK, EINVAL, EUNSUPPORTED, ELAUNCH, ENOSPACE = 0, -1, -2, -3, -4
+
+
+class CeaTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("size", ctypes.c_int64 * MAX_DIMS),
+        ("stride", ctypes.c_int64 * MAX_DIMS),
+    ]
+
+
+_P = ctypes.POINTER(CeaTensor)
+_SIGNATURES = {
+    "cea_last_error": (ctypes.c_char_p, []),
+    "cea_version": (ctypes.c_int, []),
+    "cea_attention_workspace_bytes": (
+        ctypes.c_size_t,
+        [ctypes.c_int64] * 6 + [ctypes.c_int32],
+    ),
+    "cea_attention_with_lse": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_double, ctypes.POINTER(ctypes.c_int32),
+         ctypes.c_int32, _P, _P, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t,
+         ctypes.c_void_p],
+    ),
+    "cea_merge_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
+    "cea_merge_attention_list": (ctypes.c_int, [ctypes.c_int32, _P, _P, _P, _P, ctypes.c_void_p]),
+    "cea_partitioned_attention_workspace_bytes": (
+        ctypes.c_size_t,
+        [ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)] + [ctypes.c_int64] * 5 + [ctypes.c_int32],
+    ),
+    "cea_partitioned_attention": (
+        ctypes.c_int,
+        [_P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_double,
+         ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, _P, _P, _P, _P, ctypes.c_void_p,
+         ctypes.c_size_t, ctypes.c_void_p],
+    ),
+    "cea_rmsnorm": (ctypes.c_int, [_P, _P, ctypes.c_double, _P, ctypes.c_void_p]),
+    "cea_rope_tables": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_void_p]),
+    "cea_apply_rotary": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_void_p]),
+    "cea_rmsnorm_rope": (
+        ctypes.c_int,
+        [_P, _P, ctypes.c_double, _P, _P, ctypes.c_int32, _P, ctypes.c_void_p],
+    ),
+    "cea_silu_mul": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def header_symbols(path: Path = HEADER_PATH) -> List[str]:
+    """Names of the functions the public header declares."""
+    text = path.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cea_[a-z0-9_]+)\s*\(", text)))
+
+
+def load_library(path: Optional[Path] = None):
+    """Loads (once) and returns the kernel library; raises if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        lib_path = Path(path) if path else LIB_PATH
+        if not lib_path.exists():
+            raise RuntimeError(
+                f"native kernel library {lib_path} is missing: build it with "
+                "`python __graft_entry__.py build` (or collaborative-edge-system_amd/build.py)"
+            )
+        lib = ctypes.CDLL(str(lib_path))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load_library().cea_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc == OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc == EINVAL:
+        raise ValueError(msg)
+    if rc == EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on one ROCm device (the kernels have no host path)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "collaborative-edge-system_amd runs its kernels on a ROCm GPU; got a tensor on "
+                f"{t.device}"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def tensor_arg(t: torch.Tensor) -> CeaTensor:
+    if t.dtype not in DTYPE_CODES:
+        raise NotImplementedError(f"dtype {t.dtype} is not supported by the kernels")
+    if t.dim() > MAX_DIMS:
+        raise ValueError(f"at most {MAX_DIMS} dimensions supported, got {t.dim()}")
+    a = CeaTensor()
+    a.data = t.data_ptr() if t.numel() > 0 else None
+    a.dtype = DTYPE_CODES[t.dtype]
+    a.ndim = t.dim()
+    for i in range(t.dim()):
+        a.size[i] = t.shape[i]
+        a.stride[i] = t.stride(i)
+    return a
+
+
+def tensor_array(ts: Sequence[torch.Tensor]):
+    arr = (CeaTensor * len(ts))()
+    for i, t in enumerate(ts):
+        arr[i] = tensor_arg(t)
+    return arr
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def kv_map_arg(kv_map: Optional[Sequence[int]]):
+    if kv_map is None:
+        return None, 0
+    arr = (ctypes.c_int32 * len(kv_map))(*[int(x) for x in kv_map])
+    return arr, len(kv_map)
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+__all__ = [
+    "CeaTensor",
+    "LIB_PATH",
+    "HEADER_PATH",
+    "MAX_PARTS",
+    "check",
+    "header_symbols",
+    "kv_map_arg",
+    "last_error",
+    "load_library",
+    "require_device",
+    "stream_of",
+    "tensor_arg",
+    "tensor_array",
+    "workspace",
+]

@@ -1,0 +1,430 @@
+// C ABI: argument validation, dtype/shape dispatch and workspace layout.  Every entry point
+// returns a status code; messages go to a per-thread buffer read by cea_last_error().
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "cea_kernels.hpp"
+
+namespace cea {
+
+static thread_local char g_error[1024] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+const char* last_error() { return g_error; }
+
+int check_tensor(const cea_tensor* t, const char* name, int ndim, int dtype, bool inner) {
+  CEA_REQUIRE(t != nullptr, CEA_EINVAL, "%s: missing tensor", name);
+  CEA_REQUIRE(t->ndim == ndim, CEA_EINVAL, "%s: expected %d dimensions, got %d", name, ndim,
+              t->ndim);
+  CEA_REQUIRE(dtype < 0 || t->dtype == dtype, CEA_EINVAL, "%s: expected dtype %s, got %s", name,
+              dtype_name(dtype), dtype_name(t->dtype));
+  CEA_REQUIRE(dtype_size(t->dtype) != 0, CEA_EINVAL, "%s: unknown dtype code %d", name,
+              t->dtype);
+  int64_t numel = 1;
+  for (int i = 0; i < ndim; ++i) {
+    CEA_REQUIRE(t->size[i] >= 0, CEA_EINVAL, "%s: negative size", name);
+    CEA_REQUIRE(t->size[i] <= INT32_MAX, CEA_EUNSUPPORTED, "%s: dimension %d too large", name, i);
+    numel *= t->size[i];
+  }
+  CEA_REQUIRE(numel == 0 || t->data != nullptr, CEA_EINVAL, "%s: null data pointer", name);
+  if (inner && ndim > 0 && t->size[ndim - 1] > 1)
+    CEA_REQUIRE(t->stride[ndim - 1] == 1, CEA_EINVAL, "%s: innermost stride must be 1", name);
+  return CEA_OK;
+}
+
+int make_head_map(HeadMap* m, int64_t Hq, int64_t Hkv, const int32_t* kv_map, int32_t len) {
+  memset(m, 0, sizeof(*m));
+  if (kv_map == nullptr) {
+    CEA_REQUIRE(Hkv >= 1 && Hq % Hkv == 0, CEA_EINVAL,
+                "%lld query heads cannot share %lld KV heads evenly", (long long)Hq,
+                (long long)Hkv);
+    m->group = (int32_t)(Hq / Hkv);
+    return CEA_OK;
+  }
+  CEA_REQUIRE(len == Hq, CEA_EINVAL, "kv_map must have one entry per query head");
+  bool regular = Hkv >= 1 && Hq % Hkv == 0;
+  const int64_t grp = regular ? Hq / Hkv : 0;
+  for (int64_t h = 0; h < Hq; ++h) {
+    CEA_REQUIRE(kv_map[h] >= 0 && kv_map[h] < Hkv, CEA_EINVAL,
+                "kv_map[%lld] = %d out of range for %lld KV heads", (long long)h, kv_map[h],
+                (long long)Hkv);
+    if (regular && kv_map[h] != h / grp) regular = false;
+  }
+  if (regular) {
+    m->group = (int32_t)grp;
+    return CEA_OK;
+  }
+  CEA_REQUIRE(Hq <= CEA_MAX_MAPPED_HEADS, CEA_EUNSUPPORTED,
+              "explicit kv_map supports at most %d query heads", CEA_MAX_MAPPED_HEADS);
+  m->group = 0;
+  for (int64_t h = 0; h < Hq; ++h) m->kv[h] = (int16_t)kv_map[h];
+  return CEA_OK;
+}
+
+static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+static int64_t ntiles_of(int64_t Sk) { return (Sk + kTileKeys - 1) / kTileKeys; }
+
+static size_t tile_bytes(int64_t B, int64_t Sk) {
+  return align_up((size_t)(B * ntiles_of(Sk)) * sizeof(TileInfo), 256);
+}
+
+// Builds the attention parameter block for one KV block; validates shapes and dtypes.
+static int make_attn_params(AttnParams* p, const cea_tensor* q, const cea_tensor* k,
+                            const cea_tensor* v, const cea_tensor* q_pos,
+                            const cea_tensor* k_pos, int32_t causal, double scale,
+                            const int32_t* kv_map, int32_t kv_map_len, cea_tensor* out,
+                            cea_tensor* lse, int32_t accumulate) {
+  int rc;
+  if ((rc = check_tensor(q, "q", 4, -1, true))) return rc;
+  const int dt = q->dtype;
+  CEA_REQUIRE(dt == CEA_F32 || dt == CEA_BF16 || dt == CEA_F16 || dt == CEA_F64,
+              CEA_EUNSUPPORTED, "attention: unsupported dtype %s", dtype_name(dt));
+  if ((rc = check_tensor(k, "k", 4, dt, true))) return rc;
+  if ((rc = check_tensor(v, "v", 4, dt, true))) return rc;
+  if ((rc = check_tensor(q_pos, "q_pos", 2, CEA_I64, false))) return rc;
+  if ((rc = check_tensor(k_pos, "k_pos", 2, CEA_I64, false))) return rc;
+  const int64_t B = q->size[0], Sq = q->size[1], Hq = q->size[2], D = q->size[3];
+  const int64_t Sk = k->size[1], Hkv = k->size[2];
+  CEA_REQUIRE(k->size[0] == B && v->size[0] == B && v->size[1] == Sk && v->size[2] == Hkv &&
+                  k->size[3] == D && v->size[3] == D,
+              CEA_EINVAL, "attention: k/v shapes do not match q");
+  CEA_REQUIRE(q_pos->size[0] == B && q_pos->size[1] == Sq, CEA_EINVAL,
+              "attention: q_pos must be [B, Sq]");
+  CEA_REQUIRE(k_pos->size[0] == B && k_pos->size[1] == Sk, CEA_EINVAL,
+              "attention: k_pos must be [B, Sk]");
+  const int acc = dt == CEA_F64 ? CEA_F64 : CEA_F32;
+  if ((rc = check_tensor(out, "out", 4, -1, true))) return rc;
+  CEA_REQUIRE(out->size[0] == B && out->size[1] == Sq && out->size[2] == Hq && out->size[3] == D,
+              CEA_EINVAL, "attention: out must be [B, Sq, Hq, D]");
+  if (lse) {
+    CEA_REQUIRE(out->dtype == acc, CEA_EINVAL, "attention: out must be %s when lse is returned",
+                dtype_name(acc));
+    if ((rc = check_tensor(lse, "lse", 3, acc, false))) return rc;
+    CEA_REQUIRE(lse->size[0] == B && lse->size[1] == Hq && lse->size[2] == Sq, CEA_EINVAL,
+                "attention: lse must be [B, Hq, Sq]");
+  } else {
+    CEA_REQUIRE(out->dtype == acc || out->dtype == dt, CEA_EINVAL,
+                "attention: out must be %s or %s", dtype_name(acc), dtype_name(dt));
+    CEA_REQUIRE(!accumulate, CEA_EINVAL, "attention: accumulate needs lse");
+  }
+  CEA_REQUIRE(D >= 1, CEA_EINVAL, "attention: empty head dimension");
+  memset(p, 0, sizeof(*p));
+  if ((rc = make_head_map(&p->map, Hq, Hkv, kv_map, kv_map_len))) return rc;
+  p->q = q->data; p->k = k->data; p->v = v->data;
+  p->q_pos = (const int64_t*)q_pos->data;
+  p->k_pos = (const int64_t*)k_pos->data;
+  p->out = out->data;
+  p->lse = lse ? lse->data : nullptr;
+  p->B = (int32_t)B; p->Sq = (int32_t)Sq; p->Hq = (int32_t)Hq;
+  p->Sk = (int32_t)Sk; p->Hkv = (int32_t)Hkv; p->D = (int32_t)D;
+  p->qs_b = q->stride[0]; p->qs_s = q->stride[1]; p->qs_h = q->stride[2];
+  p->ks_b = k->stride[0]; p->ks_s = k->stride[1]; p->ks_h = k->stride[2];
+  p->vs_b = v->stride[0]; p->vs_s = v->stride[1]; p->vs_h = v->stride[2];
+  p->qps_b = q_pos->stride[0]; p->qps_s = q_pos->stride[1];
+  p->kps_b = k_pos->stride[0]; p->kps_s = k_pos->stride[1];
+  p->os_b = out->stride[0]; p->os_s = out->stride[1]; p->os_h = out->stride[2];
+  if (lse) { p->ls_b = lse->stride[0]; p->ls_h = lse->stride[1]; p->ls_s = lse->stride[2]; }
+  p->scale = scale;
+  p->causal = causal ? 1 : 0;
+  p->accumulate = accumulate ? 1 : 0;
+  p->in_dtype = dt;
+  p->out_dtype = out->dtype;
+  p->ntiles = (int32_t)ntiles_of(Sk);
+  return CEA_OK;
+}
+
+// Runs one attention call with a prepared parameter block.
+static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t st) {
+  if (p.Sk > 0 && prefill_mfma_supported(p)) {
+    const size_t need = tile_bytes(p.B, p.Sk);
+    CEA_REQUIRE(ws != nullptr && ws_bytes >= need, CEA_ENOSPACE,
+                "attention: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+    p.tiles = (const TileInfo*)ws;
+    int rc = launch_tile_info(p.k_pos, p.kps_b, p.kps_s, p.B, p.Sk, (TileInfo*)ws, p.ntiles, st);
+    if (rc) return rc;
+    return launch_attn_prefill_mfma(p, st);
+  }
+  return launch_attn_generic(p, st);
+}
+
+}  // namespace cea
+
+using namespace cea;
+
+extern "C" {
+
+const char* cea_last_error(void) { return cea::last_error(); }
+
+int cea_version(void) { return 100; }
+
+size_t cea_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int64_t Hkv,
+                                     int64_t D, int32_t in_dtype) {
+  (void)Sq; (void)Hq; (void)Hkv; (void)D; (void)in_dtype;
+  if (B <= 0 || Sk <= 0) return 256;
+  return tile_bytes(B, Sk);
+}
+
+int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
+                           const cea_tensor* q_pos, const cea_tensor* k_pos, int32_t causal,
+                           double scale, const int32_t* kv_map, int32_t kv_map_len,
+                           cea_tensor* out, cea_tensor* lse, int32_t accumulate,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  AttnParams p;
+  int rc = make_attn_params(&p, q, k, v, q_pos, k_pos, causal, scale, kv_map, kv_map_len, out,
+                            lse, accumulate);
+  if (rc) return rc;
+  return run_attention(p, (char*)workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+static int fill_merge_part(MergeParams* m, int i, const cea_tensor* o, const cea_tensor* l,
+                           int64_t B, int64_t Sq, int64_t H, int64_t D, int dt) {
+  int rc;
+  if ((rc = check_tensor(o, "out_i", 4, dt, true))) return rc;
+  if ((rc = check_tensor(l, "lse_i", 3, dt, false))) return rc;
+  CEA_REQUIRE(o->size[0] == B && o->size[1] == Sq && o->size[2] == H && o->size[3] == D,
+              CEA_EINVAL, "merge: partial %d has a different output shape", i);
+  CEA_REQUIRE(l->size[0] == B && l->size[1] == H && l->size[2] == Sq, CEA_EINVAL,
+              "merge: partial %d lse must be [B, H, Sq]", i);
+  m->outs[i] = o->data;
+  m->lses[i] = l->data;
+  for (int j = 0; j < 3; ++j) {
+    m->os[i][j] = o->stride[j];
+    m->ls[i][j] = l->stride[j];
+  }
+  return CEA_OK;
+}
+
+static int merge_impl(int32_t n, const cea_tensor* outs, const cea_tensor* lses, cea_tensor* out,
+                      cea_tensor* lse, int pairwise, hipStream_t st) {
+  CEA_REQUIRE(n >= 1 && n <= CEA_MAX_PARTS, CEA_EUNSUPPORTED,
+              "merge: between 1 and %d partial results supported, got %d", CEA_MAX_PARTS, n);
+  int rc;
+  if ((rc = check_tensor(&outs[0], "out_0", 4, -1, true))) return rc;
+  const int dt = outs[0].dtype;
+  CEA_REQUIRE(dt == CEA_F32 || dt == CEA_F64, CEA_EUNSUPPORTED,
+              "merge: partial results must be float32 or float64, got %s", dtype_name(dt));
+  const int64_t B = outs[0].size[0], Sq = outs[0].size[1], H = outs[0].size[2],
+                D = outs[0].size[3];
+  MergeParams m;
+  memset(&m, 0, sizeof(m));
+  m.n = n;
+  m.pairwise = pairwise;
+  m.B = (int32_t)B; m.Sq = (int32_t)Sq; m.H = (int32_t)H; m.D = (int32_t)D;
+  m.dtype = dt;
+  for (int i = 0; i < n; ++i)
+    if ((rc = fill_merge_part(&m, i, &outs[i], &lses[i], B, Sq, H, D, dt))) return rc;
+  if ((rc = check_tensor(out, "out", 4, -1, true))) return rc;
+  CEA_REQUIRE(out->dtype == dt || (dt == CEA_F32 && (out->dtype == CEA_BF16 ||
+                                                     out->dtype == CEA_F16)),
+              CEA_EINVAL, "merge: output dtype %s not allowed for %s partials",
+              dtype_name(out->dtype), dtype_name(dt));
+  CEA_REQUIRE(out->size[0] == B && out->size[1] == Sq && out->size[2] == H && out->size[3] == D,
+              CEA_EINVAL, "merge: out must be [B, Sq, H, D]");
+  m.out_dtype = out->dtype;
+  m.out = out->data;
+  for (int j = 0; j < 3; ++j) m.dos[j] = out->stride[j];
+  if (lse) {
+    if ((rc = check_tensor(lse, "lse", 3, dt, false))) return rc;
+    CEA_REQUIRE(lse->size[0] == B && lse->size[1] == H && lse->size[2] == Sq, CEA_EINVAL,
+                "merge: lse must be [B, H, Sq]");
+    m.lse = lse->data;
+    for (int j = 0; j < 3; ++j) m.dls[j] = lse->stride[j];
+  }
+  return launch_merge(m, st);
+}
+
+int cea_merge_attention(const cea_tensor* out_a, const cea_tensor* lse_a, const cea_tensor* out_b,
+                        const cea_tensor* lse_b, cea_tensor* out, cea_tensor* lse, void* stream) {
+  CEA_REQUIRE(out_a && lse_a && out_b && lse_b && lse, CEA_EINVAL, "merge: missing tensor");
+  cea_tensor outs[2] = {*out_a, *out_b};
+  cea_tensor lses[2] = {*lse_a, *lse_b};
+  return merge_impl(2, outs, lses, out, lse, 1, (hipStream_t)stream);
+}
+
+int cea_merge_attention_list(int32_t n, const cea_tensor* outs, const cea_tensor* lses,
+                             cea_tensor* out, cea_tensor* lse, void* stream) {
+  CEA_REQUIRE(outs && lses && lse, CEA_EINVAL, "merge: missing tensor");
+  return merge_impl(n, outs, lses, out, lse, 0, (hipStream_t)stream);
+}
+
+size_t cea_partitioned_attention_workspace_bytes(int32_t n, const int64_t* Sk, int64_t B,
+                                                 int64_t Sq, int64_t Hq, int64_t Hkv, int64_t D,
+                                                 int32_t in_dtype) {
+  (void)Hkv;
+  if (n <= 0 || n > CEA_MAX_PARTS || B <= 0) return 256;
+  const size_t esz = in_dtype == CEA_F64 ? 8 : 4;
+  size_t need = 0;
+  int64_t maxsk = 0;
+  for (int i = 0; i < n; ++i) maxsk = Sk[i] > maxsk ? Sk[i] : maxsk;
+  need += tile_bytes(B, maxsk);
+  // per-partition partials (out, lse) in the accumulation dtype
+  need += (size_t)n * align_up((size_t)(B * Sq * Hq * D) * esz, 256);
+  need += (size_t)n * align_up((size_t)(B * Hq * Sq) * esz, 256);
+  return need;
+}
+
+int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* ks,
+                              const cea_tensor* vs, const cea_tensor* q_pos,
+                              const cea_tensor* k_pos_s, int32_t causal, double scale,
+                              const int32_t* kv_map, int32_t kv_map_len, cea_tensor* part_out,
+                              cea_tensor* part_lse, cea_tensor* out, cea_tensor* lse,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  CEA_REQUIRE(n >= 1 && n <= CEA_MAX_PARTS, CEA_EUNSUPPORTED,
+              "partitioned attention: between 1 and %d partitions supported, got %d",
+              CEA_MAX_PARTS, n);
+  CEA_REQUIRE(q && ks && vs && q_pos && k_pos_s && out, CEA_EINVAL,
+              "partitioned attention: missing tensor");
+  CEA_REQUIRE((part_out == nullptr) == (part_lse == nullptr), CEA_EINVAL,
+              "partitioned attention: part_out and part_lse go together");
+  hipStream_t st = (hipStream_t)stream;
+  int rc = check_tensor(q, "q", 4, -1, true);
+  if (rc) return rc;
+  CEA_REQUIRE(q->dtype != CEA_F64 || out->dtype == CEA_F64, CEA_EINVAL,
+              "partitioned attention: float64 inputs need a float64 output");
+  const int64_t B = q->size[0], Sq = q->size[1], Hq = q->size[2], D = q->size[3];
+  const int acc = q->dtype == CEA_F64 ? CEA_F64 : CEA_F32;
+  const size_t esz = acc == CEA_F64 ? 8 : 4;
+  int64_t sks[CEA_MAX_PARTS];
+  for (int i = 0; i < n; ++i) sks[i] = ks[i].size[1];
+  const size_t need = cea_partitioned_attention_workspace_bytes(n, sks, B, Sq, Hq, ks[0].size[2],
+                                                                D, q->dtype);
+  CEA_REQUIRE(workspace != nullptr && workspace_bytes >= need, CEA_ENOSPACE,
+              "partitioned attention: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+  char* ws = (char*)workspace;
+  int64_t maxsk = 0;
+  for (int i = 0; i < n; ++i) maxsk = sks[i] > maxsk ? sks[i] : maxsk;
+  char* tiles = ws;
+  char* parts = ws + tile_bytes(B, maxsk);
+  const size_t obytes = align_up((size_t)(B * Sq * Hq * D) * esz, 256);
+  const size_t lbytes = align_up((size_t)(B * Hq * Sq) * esz, 256);
+
+  cea_tensor po[CEA_MAX_PARTS], pl[CEA_MAX_PARTS];
+  for (int i = 0; i < n; ++i) {
+    if (part_out) {
+      po[i] = part_out[i];
+      pl[i] = part_lse[i];
+    } else {
+      cea_tensor& o = po[i];
+      cea_tensor& l = pl[i];
+      o.data = parts + i * obytes;
+      o.dtype = acc; o.ndim = 4;
+      o.size[0] = B; o.size[1] = Sq; o.size[2] = Hq; o.size[3] = D;
+      o.stride[3] = 1; o.stride[2] = D; o.stride[1] = Hq * D; o.stride[0] = Sq * Hq * D;
+      l.data = parts + n * obytes + i * lbytes;
+      l.dtype = acc; l.ndim = 3;
+      l.size[0] = B; l.size[1] = Hq; l.size[2] = Sq;
+      l.stride[2] = 1; l.stride[1] = Sq; l.stride[0] = Hq * Sq;
+    }
+    AttnParams p;
+    rc = make_attn_params(&p, q, &ks[i], &vs[i], q_pos, &k_pos_s[i], causal, scale, kv_map,
+                          kv_map_len, &po[i], &pl[i], 0);
+    if (rc) return rc;
+    rc = run_attention(p, tiles, tile_bytes(B, maxsk), st);
+    if (rc) return rc;
+  }
+  if (n == 1 && out->data == po[0].data) return CEA_OK;
+  return merge_impl(n, po, pl, out, lse, 0, st);
+}
+
+int cea_rmsnorm(const cea_tensor* x, const cea_tensor* weight, double eps, cea_tensor* y,
+                void* stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 2, -1, true))) return rc;
+  if ((rc = check_tensor(weight, "weight", 1, -1, true))) return rc;
+  if ((rc = check_tensor(y, "y", 2, -1, true))) return rc;
+  CEA_REQUIRE(weight->size[0] == x->size[1], CEA_EINVAL, "rmsnorm: weight must be [C]");
+  CEA_REQUIRE(y->size[0] == x->size[0] && y->size[1] == x->size[1], CEA_EINVAL,
+              "rmsnorm: y must match x");
+  return launch_rmsnorm(x, weight, eps, y, (hipStream_t)stream);
+}
+
+int cea_rope_tables(const cea_tensor* positions, const cea_tensor* inv_freq, cea_tensor* cos,
+                    cea_tensor* sin, void* stream) {
+  int rc;
+  if ((rc = check_tensor(positions, "positions", 2, CEA_I64, false))) return rc;
+  if ((rc = check_tensor(inv_freq, "inv_freq", 1, -1, true))) return rc;
+  if ((rc = check_tensor(cos, "cos", 3, -1, true))) return rc;
+  if ((rc = check_tensor(sin, "sin", 3, cos->dtype, true))) return rc;
+  const int want = cos->dtype == CEA_F64 ? CEA_F64 : CEA_F32;
+  CEA_REQUIRE(inv_freq->dtype == want, CEA_EINVAL, "rope_tables: inv_freq must be %s",
+              dtype_name(want));
+  const int64_t half = inv_freq->size[0];
+  for (const cea_tensor* t : {(const cea_tensor*)cos, (const cea_tensor*)sin})
+    CEA_REQUIRE(t->size[0] == positions->size[0] && t->size[1] == positions->size[1] &&
+                    t->size[2] == 2 * half,
+                CEA_EINVAL, "rope_tables: tables must be [B, S, 2*len(inv_freq)]");
+  return launch_rope_tables(positions, inv_freq, cos, sin, (hipStream_t)stream);
+}
+
+int cea_apply_rotary(const cea_tensor* x, const cea_tensor* cos, const cea_tensor* sin,
+                     cea_tensor* out, void* stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 4, -1, true))) return rc;
+  if ((rc = check_tensor(cos, "cos", 3, x->dtype, true))) return rc;
+  if ((rc = check_tensor(sin, "sin", 3, x->dtype, true))) return rc;
+  if ((rc = check_tensor(out, "out", 4, x->dtype, true))) return rc;
+  const int64_t D = x->size[3];
+  CEA_REQUIRE(D % 2 == 0, CEA_EINVAL, "apply_rotary: head size must be even");
+  for (const cea_tensor* t : {cos, sin})
+    CEA_REQUIRE((t->size[0] == x->size[0] || (t->size[0] == 1 && t->stride[0] == 0) ||
+                 t->size[0] == 1) &&
+                    t->size[1] == x->size[1] && t->size[2] == D,
+                CEA_EINVAL, "apply_rotary: cos/sin must be [B, S, D]");
+  for (int i = 0; i < 4; ++i)
+    CEA_REQUIRE(out->size[i] == x->size[i], CEA_EINVAL, "apply_rotary: out must match x");
+  cea_tensor c = *cos, s = *sin;
+  if (c.size[0] == 1) c.stride[0] = 0;  // broadcast over the batch
+  if (s.size[0] == 1) s.stride[0] = 0;
+  return launch_apply_rotary(x, &c, &s, out, (hipStream_t)stream);
+}
+
+int cea_rmsnorm_rope(const cea_tensor* x, const cea_tensor* weight, double eps,
+                     const cea_tensor* positions, const cea_tensor* inv_freq, int32_t num_heads,
+                     cea_tensor* out, void* stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 2, -1, true))) return rc;
+  if ((rc = check_tensor(weight, "weight", 1, x->dtype, true))) return rc;
+  if ((rc = check_tensor(out, "out", 2, x->dtype, true))) return rc;
+  CEA_REQUIRE(positions && (positions->ndim == 1 || positions->ndim == 2) &&
+                  positions->dtype == CEA_I64,
+              CEA_EINVAL, "rmsnorm_rope: positions must be int64 [S] or [1, S]");
+  const int64_t S = x->size[0], C = x->size[1];
+  const int64_t npos = positions->ndim == 2 ? positions->size[1] : positions->size[0];
+  CEA_REQUIRE(positions->ndim == 1 || positions->size[0] == 1, CEA_EINVAL,
+              "rmsnorm_rope: positions must have batch 1");
+  CEA_REQUIRE(npos == S, CEA_EINVAL, "rmsnorm_rope: one position per row needed");
+  CEA_REQUIRE(num_heads >= 1 && C % num_heads == 0, CEA_EINVAL,
+              "rmsnorm_rope: %lld features do not split into %d heads", (long long)C, num_heads);
+  const int64_t D = C / num_heads;
+  CEA_REQUIRE(D % 2 == 0 && D <= 1024, CEA_EUNSUPPORTED,
+              "rmsnorm_rope: head size %lld must be even and <= 1024", (long long)D);
+  CEA_REQUIRE(weight->size[0] == C, CEA_EINVAL, "rmsnorm_rope: weight must be [C]");
+  CEA_REQUIRE(out->size[0] == S && out->size[1] == C, CEA_EINVAL, "rmsnorm_rope: out must match x");
+  if ((rc = check_tensor(inv_freq, "inv_freq", 1, x->dtype == CEA_F64 ? CEA_F64 : CEA_F32, true)))
+    return rc;
+  CEA_REQUIRE(inv_freq->size[0] == D / 2, CEA_EINVAL, "rmsnorm_rope: inv_freq must be [D/2]");
+  return launch_rmsnorm_rope(x, weight, eps, positions, inv_freq, num_heads, out,
+                             (hipStream_t)stream);
+}
+
+int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, void* stream) {
+  int rc;
+  if ((rc = check_tensor(gate, "gate", 2, -1, true))) return rc;
+  if ((rc = check_tensor(up, "up", 2, gate->dtype, true))) return rc;
+  if ((rc = check_tensor(out, "out", 2, gate->dtype, true))) return rc;
+  for (int i = 0; i < 2; ++i)
+    CEA_REQUIRE(up->size[i] == gate->size[i] && out->size[i] == gate->size[i], CEA_EINVAL,
+                "silu_mul: gate, up and out must have the same shape");
+  return launch_silu_mul(gate, up, out, (hipStream_t)stream);
+}
+
+}  // extern "C"

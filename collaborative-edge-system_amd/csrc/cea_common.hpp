@@ -1,0 +1,195 @@
+// Shared helpers of the gfx950 kernels: element types, rounding, wavefront reductions,
+// error reporting and tensor-argument validation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+#include <string>
+
+#include "collab_edge_attn.h"
+
+namespace cea {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+// ---------------------------------------------------------------------------------------
+// error reporting (one message per host thread)
+// ---------------------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+const char* last_error();
+
+#define CEA_REQUIRE(cond, code, ...)   \
+  do {                                 \
+    if (!(cond)) {                     \
+      ::cea::set_error(__VA_ARGS__);   \
+      return (code);                   \
+    }                                  \
+  } while (0)
+
+#define CEA_CHECK_LAUNCH(what)                                                    \
+  do {                                                                            \
+    hipError_t _e = hipGetLastError();                                            \
+    if (_e != hipSuccess) {                                                       \
+      ::cea::set_error("%s: launch failed: %s", (what), hipGetErrorString(_e));   \
+      return CEA_ELAUNCH;                                                         \
+    }                                                                             \
+  } while (0)
+
+inline size_t dtype_size(int32_t dt) {
+  switch (dt) {
+    case CEA_F32: return 4;
+    case CEA_BF16: return 2;
+    case CEA_F16: return 2;
+    case CEA_F64: return 8;
+    case CEA_I64: return 8;
+    default: return 0;
+  }
+}
+
+inline const char* dtype_name(int32_t dt) {
+  switch (dt) {
+    case CEA_F32: return "float32";
+    case CEA_BF16: return "bfloat16";
+    case CEA_F16: return "float16";
+    case CEA_F64: return "float64";
+    case CEA_I64: return "int64";
+    default: return "unknown";
+  }
+}
+
+// Checks rank, dtype and (optionally) a unit innermost stride.  Returns 0 or an error code.
+int check_tensor(const cea_tensor* t, const char* name, int ndim, int dtype_or_minus1,
+                 bool inner_contiguous);
+
+// ---------------------------------------------------------------------------------------
+// device-side element conversion
+// ---------------------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
+template <> __device__ __forceinline__ float to_f32<bf16>(bf16 x) {
+  return __uint_as_float(((uint32_t)__builtin_bit_cast(uint16_t, x)) << 16);
+}
+
+// Round-to-nearest-even conversions (hardware v_cvt_pk_bf16_f32 / v_cvt_f16_f32).
+template <typename T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
+template <typename T> __device__ __forceinline__ T from_f64(double x) { return (T)x; }
+
+// x rounded to the storage type T and widened back to float: the value a torch op
+// producing a T tensor would hand to the next op.
+template <typename T> __device__ __forceinline__ float round_to(float x) {
+  return to_f32<T>(from_f32<T>(x));
+}
+template <> __device__ __forceinline__ float round_to<float>(float x) { return x; }
+
+// Accumulation type: f64 for f64 inputs, f32 otherwise (attention.py:56-57).
+template <typename T> struct acc_of { typedef float type; };
+template <> struct acc_of<double> { typedef double type; };
+
+template <typename A> __device__ __forceinline__ A neg_inf();
+template <> __device__ __forceinline__ float neg_inf<float>() { return -__builtin_inff(); }
+template <> __device__ __forceinline__ double neg_inf<double>() { return -__builtin_inf(); }
+
+// Element load widened to the accumulation type.
+template <typename T, typename A> __device__ __forceinline__ A load_acc(const T* p) {
+  return (A)to_f32<T>(*p);
+}
+template <> __device__ __forceinline__ double load_acc<double, double>(const double* p) {
+  return *p;
+}
+template <> __device__ __forceinline__ float load_acc<float, float>(const float* p) { return *p; }
+
+template <typename T, typename A> __device__ __forceinline__ T store_cast(A x) { return (T)x; }
+template <> __device__ __forceinline__ bf16 store_cast<bf16, float>(float x) { return (bf16)x; }
+template <> __device__ __forceinline__ bf16 store_cast<bf16, double>(double x) {
+  return (bf16)(float)x;  // f64 results are only stored as f64; kept for completeness
+}
+
+// Exact-rounding arithmetic without contraction into FMA, to follow the reference's
+// separately rounded tensor ops.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ double mul_rn(double a, double b) { return __dmul_rn(a, b); }
+__device__ __forceinline__ double add_rn(double a, double b) { return __dadd_rn(a, b); }
+__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+__device__ __forceinline__ double div_rn(double a, double b) { return __ddiv_rn(a, b); }
+
+__device__ __forceinline__ float exp_acc(float x) { return expf(x); }
+__device__ __forceinline__ double exp_acc(double x) { return exp(x); }
+__device__ __forceinline__ float log_acc(float x) { return logf(x); }
+__device__ __forceinline__ double log_acc(double x) { return log(x); }
+__device__ __forceinline__ float log1p_acc(float x) { return log1pf(x); }
+__device__ __forceinline__ double log1p_acc(double x) { return log1p(x); }
+__device__ __forceinline__ bool is_finite(float x) { return __builtin_isfinite(x); }
+__device__ __forceinline__ bool is_finite(double x) { return __builtin_isfinite(x); }
+__device__ __forceinline__ bool is_inf(float x) { return __builtin_isinf(x); }
+__device__ __forceinline__ bool is_inf(double x) { return __builtin_isinf(x); }
+
+// torch.logaddexp semantics: equal infinities return that infinity, otherwise
+// max + log1p(exp(-|a-b|)).
+template <typename A> __device__ __forceinline__ A logaddexp(A a, A b) {
+  if (is_inf(a) && a == b) return a;
+  A m = a > b ? a : b;
+  A d = a > b ? a - b : b - a;
+  return m + log1p_acc(exp_acc(-d));
+}
+
+// ---------------------------------------------------------------------------------------
+// wavefront (64-lane) reductions
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ int64_t wave_min_i64(int64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    int64_t o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    int64_t o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Uniform (scalar) copy of a wave-uniform value.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// ---------------------------------------------------------------------------------------
+// key-tile position summary used to skip or classify KV tiles without host syncs
+// ---------------------------------------------------------------------------------------
+struct TileInfo {
+  int64_t min_valid;  // smallest k_pos >= 0 in the tile (INT64_MAX if none)
+  int64_t max_valid;  // largest  k_pos >= 0 in the tile (INT64_MIN if none)
+  int32_t n_valid;    // number of keys with k_pos >= 0 (keys past Sk count as invalid)
+  int32_t pad[3];
+};
+static_assert(sizeof(TileInfo) == 32, "TileInfo must stay 32 bytes");
+
+// Query-head -> KV-head mapping passed by value to the kernels.
+struct HeadMap {
+  int32_t group;  // > 0: kv = h / group; 0: explicit table
+  int16_t kv[CEA_MAX_MAPPED_HEADS];
+  __device__ __forceinline__ int kv_of(int h) const { return group > 0 ? h / group : kv[h]; }
+};
+
+int make_head_map(HeadMap* m, int64_t Hq, int64_t Hkv, const int32_t* kv_map, int32_t len);
+
+}  // namespace cea

@@ -1,0 +1,113 @@
+// Parameter blocks and launcher declarations shared between the C ABI (capi.hip) and the
+// kernel translation units.  Sizes are validated on the host before any launch.
+#pragma once
+
+#include "cea_common.hpp"
+
+namespace cea {
+
+// One attention call: query block [B,Sq,Hq,D] against one KV block [B,Sk,Hkv,D].
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int64_t* q_pos;
+  const int64_t* k_pos;
+  void* out;
+  void* lse;                 // may be null (plain attention)
+  const TileInfo* tiles;     // [B, ntiles] summaries of k_pos (prefill kernels)
+  int32_t B, Sq, Hq, Sk, Hkv, D;
+  int64_t qs_b, qs_s, qs_h;  // element strides
+  int64_t ks_b, ks_s, ks_h;
+  int64_t vs_b, vs_s, vs_h;
+  int64_t qps_b, qps_s;
+  int64_t kps_b, kps_s;
+  int64_t os_b, os_s, os_h;
+  int64_t ls_b, ls_h, ls_s;
+  double scale;
+  int32_t causal;
+  int32_t accumulate;        // merge into existing (out, lse)
+  int32_t in_dtype;
+  int32_t out_dtype;
+  int32_t ntiles;
+  HeadMap map;
+};
+
+// n-way merge of partial results (n <= CEA_MAX_PARTS).
+struct MergeParams {
+  int32_t n;
+  int32_t pairwise;          // 1: logaddexp of two partials (merge_attention), 0: logsumexp
+  int32_t B, Sq, H, D;
+  int32_t dtype;             // partial dtype: CEA_F32 or CEA_F64
+  int32_t out_dtype;         // merged output: the partial dtype, or bf16/f16 from f32
+  const void* outs[CEA_MAX_PARTS];
+  const void* lses[CEA_MAX_PARTS];
+  int64_t os[CEA_MAX_PARTS][3];   // b, s, h strides
+  int64_t ls[CEA_MAX_PARTS][3];   // b, h, s strides
+  void* out;
+  void* lse;
+  int64_t dos[3];
+  int64_t dls[3];
+};
+
+// Split-KV decode over one or more KV partitions (short query blocks).
+struct DecodeParams {
+  int32_t nparts;
+  const void* q;
+  const int64_t* q_pos;
+  int32_t B, Sq, Hq, Hkv, D;
+  int64_t qs_b, qs_s, qs_h;
+  int64_t qps_b, qps_s;
+  const void* k[CEA_MAX_PARTS];
+  const void* v[CEA_MAX_PARTS];
+  const int64_t* k_pos[CEA_MAX_PARTS];
+  int32_t Sk[CEA_MAX_PARTS];
+  int64_t ks[CEA_MAX_PARTS][3];
+  int64_t vs[CEA_MAX_PARTS][3];
+  int64_t kps[CEA_MAX_PARTS][2];
+  int32_t chunk_begin[CEA_MAX_PARTS + 1];  // prefix sum of key chunks per partition
+  int32_t chunk;                            // keys per chunk
+  double scale;
+  int32_t causal;
+  int32_t in_dtype;
+  HeadMap map;
+  // partial results [B, Hkv, total_chunks, G, Sq] x {D + 2} floats (o unnormalised, m, l)
+  float* partial;
+  int32_t G;                 // query heads per KV head handled by one work item
+  // outputs of the reduction
+  void* part_out[CEA_MAX_PARTS];   // optional per-partition (out, lse), f32
+  void* part_lse[CEA_MAX_PARTS];
+  int64_t pos_[CEA_MAX_PARTS][3];  // per-partition out strides (b, s, h)
+  int64_t pls_[CEA_MAX_PARTS][3];  // per-partition lse strides (b, h, s)
+  void* out;
+  void* lse;
+  int64_t os_b, os_s, os_h;
+  int64_t ls_b, ls_h, ls_s;
+  int32_t out_dtype;
+  int32_t accumulate;
+};
+
+int launch_merge(const MergeParams& p, hipStream_t s);
+int launch_rmsnorm(const cea_tensor* x, const cea_tensor* w, double eps, cea_tensor* y,
+                   hipStream_t s);
+int launch_rope_tables(const cea_tensor* pos, const cea_tensor* inv, cea_tensor* c,
+                       cea_tensor* sn, hipStream_t s);
+int launch_apply_rotary(const cea_tensor* x, const cea_tensor* c, const cea_tensor* sn,
+                        cea_tensor* o, hipStream_t s);
+int launch_rmsnorm_rope(const cea_tensor* x, const cea_tensor* w, double eps,
+                        const cea_tensor* pos, const cea_tensor* inv, int H, cea_tensor* o,
+                        hipStream_t s);
+int launch_silu_mul(const cea_tensor* g, const cea_tensor* u, cea_tensor* o, hipStream_t s);
+int launch_attn_generic(const AttnParams& p, hipStream_t s);
+int launch_tile_info(const int64_t* k_pos, int64_t kps_b, int64_t kps_s, int32_t B, int32_t Sk,
+                     TileInfo* tiles, int32_t ntiles, hipStream_t s);
+bool prefill_mfma_supported(const AttnParams& p);
+int launch_attn_prefill_mfma(const AttnParams& p, hipStream_t s);
+bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype,
+                      const HeadMap& map);
+int decode_plan_chunk(int64_t total_keys, int32_t B, int32_t Hkv);
+int launch_attn_decode(const DecodeParams& p, hipStream_t s);
+
+constexpr int kTileKeys = 64;  // keys per KV tile of the prefill kernels / tile summaries
+
+}  // namespace cea

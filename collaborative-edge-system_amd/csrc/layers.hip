@@ -1,0 +1,522 @@
+// LLaMA-family layer ops, HBM-bound, with the reference's rounding points.
+//
+//   RMSNorm        collab_infer/models/llama.py:52-61
+//   rotary tables  collab_infer/models/llama.py:64-77 (inv_freq: models/config.py:165-189)
+//   apply_rotary   collab_infer/models/llama.py:80-88 (half-split, NeoX/HF convention)
+//   SiLU-gate      collab_infer/models/llama.py:45, 305, 316
+//
+// Rounding: the reference runs separate tensor ops, each rounding to the tensor dtype.  The
+// kernels keep every such rounding point (x*r -> T, w*that -> out dtype; x*cos -> T,
+// rot*sin -> T, sum -> T; silu -> T, silu*up -> T) and compute between them in f32
+// (f64 for f64 tensors), so a fused kernel returns what the op sequence returns.
+#include "cea_kernels.hpp"
+
+namespace cea {
+
+// ---------------------------------------------------------------------------------------
+// vector I/O: VEC elements of T as one 16-byte access when VEC * sizeof(T) == 16
+// ---------------------------------------------------------------------------------------
+template <typename T, int VEC> struct Vec {
+  T v[VEC];
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec(const T* p, T (&out)[VEC]) {
+  if constexpr (VEC * sizeof(T) == 16) {
+    const uint4 raw = *(const uint4*)p;
+    __builtin_memcpy(out, &raw, 16);
+  } else if constexpr (VEC * sizeof(T) == 8) {
+    const uint2 raw = *(const uint2*)p;
+    __builtin_memcpy(out, &raw, 8);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[e] = p[e];
+  }
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_vec(T* p, const T (&in)[VEC]) {
+  if constexpr (VEC * sizeof(T) == 16) {
+    uint4 raw;
+    __builtin_memcpy(&raw, in, 16);
+    *(uint4*)p = raw;
+  } else if constexpr (VEC * sizeof(T) == 8) {
+    uint2 raw;
+    __builtin_memcpy(&raw, in, 8);
+    *(uint2*)p = raw;
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) p[e] = in[e];
+  }
+}
+
+template <typename T> struct math_of { typedef float type; };
+template <> struct math_of<double> { typedef double type; };
+
+template <typename T, typename M> __device__ __forceinline__ M widen(T x) {
+  return (M)to_f32<T>(x);
+}
+template <> __device__ __forceinline__ double widen<double, double>(double x) { return x; }
+
+template <typename T, typename M> __device__ __forceinline__ T narrow(M x) { return (T)x; }
+
+// value after a round trip through T (identity when T is the math type)
+template <typename T, typename M> __device__ __forceinline__ M rnd(M x) {
+  if constexpr (sizeof(T) == sizeof(M)) return x;
+  else return widen<T, M>(narrow<T, M>(x));
+}
+
+__device__ __forceinline__ float rsqrt_rn(float v) { return __fdiv_rn(1.0f, __fsqrt_rn(v)); }
+__device__ __forceinline__ double rsqrt_rn(double v) { return __ddiv_rn(1.0, __dsqrt_rn(v)); }
+
+template <typename M> __device__ __forceinline__ M block_sum_256(M v, M* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  M t = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return t;
+}
+
+// ---------------------------------------------------------------------------------------
+// RMSNorm: one 256-thread block per row; NV vectors per thread stay in registers between
+// the reduction and the scaling pass (rows of up to 256*VEC*NV elements).
+// ---------------------------------------------------------------------------------------
+template <typename T, typename W, typename O, int VEC, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x, int64_t xs,
+                                                      const W* __restrict__ w,
+                                                      O* __restrict__ y, int64_t ys, int C,
+                                                      double eps_d) {
+  typedef typename math_of<T>::type M;
+  __shared__ M red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * xs;
+  O* yr = y + row * ys;
+  T cache[NV][VEC];
+  M ss = 0;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 256 + threadIdx.x) * VEC;
+    if (c < C) {
+      load_vec<T, VEC>(xr + c, cache[i]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const M h = widen<T, M>(cache[i][e]);
+        ss += h * h;
+      }
+    }
+  }
+  for (int c = (NV * 256 + threadIdx.x) * VEC; c < C; c += 256 * VEC) {
+    T tmp[VEC];
+    load_vec<T, VEC>(xr + c, tmp);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const M h = widen<T, M>(tmp[e]);
+      ss += h * h;
+    }
+  }
+  ss = block_sum_256<M>(ss, red);
+  const M eps = (M)eps_d;
+  const M r = rsqrt_rn(add_rn(div_rn(ss, (M)C), eps));
+
+  auto emit = [&](int c, const T (&xv)[VEC]) {
+    W wv[VEC];
+    load_vec<W, VEC>(w + c, wv);
+    O ov[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const M yn = rnd<T, M>(mul_rn(widen<T, M>(xv[e]), r));  // (x * r).to(x.dtype)
+      ov[e] = narrow<O, M>(mul_rn(widen<W, M>(wv[e]), yn));  // weight * that
+    }
+    store_vec<O, VEC>(yr + c, ov);
+  };
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 256 + threadIdx.x) * VEC;
+    if (c < C) emit(c, cache[i]);
+  }
+  for (int c = (NV * 256 + threadIdx.x) * VEC; c < C; c += 256 * VEC) {
+    T tmp[VEC];
+    load_vec<T, VEC>(xr + c, tmp);
+    emit(c, tmp);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// rotary tables
+// ---------------------------------------------------------------------------------------
+template <typename M> __device__ __forceinline__ M pos_to(int64_t p) {
+  return (M)(p < 0 ? 0 : p);  // positions.clamp(min=0).to(inv_freq.dtype)
+}
+__device__ __forceinline__ void sincos_acc(float a, float* s, float* c) {
+  *s = sinf(a);
+  *c = cosf(a);
+}
+__device__ __forceinline__ void sincos_acc(double a, double* s, double* c) {
+  *s = sin(a);
+  *c = cos(a);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rope_tables_kernel(
+    const int64_t* __restrict__ pos, int64_t ps_b, int64_t ps_s,
+    const typename math_of<T>::type* __restrict__ inv_freq, T* __restrict__ cosb,
+    T* __restrict__ sinb, int64_t cs_b, int64_t cs_s, int64_t ss_b, int64_t ss_s, int B, int S,
+    int half) {
+  typedef typename math_of<T>::type M;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)B * S * half;
+  if (t >= total) return;
+  const int j = (int)(t % half);
+  const int64_t bs = t / half;
+  const int s = (int)(bs % S);
+  const int b = (int)(bs / S);
+  const M f = mul_rn(pos_to<M>(pos[b * ps_b + s * ps_s]), inv_freq[j]);
+  M sv, cv;
+  sincos_acc(f, &sv, &cv);
+  const T c = narrow<T, M>(cv), sn = narrow<T, M>(sv);
+  T* cp = cosb + b * cs_b + s * cs_s;
+  T* sp = sinb + b * ss_b + s * ss_s;
+  cp[j] = c;
+  cp[j + half] = c;
+  sp[j] = sn;
+  sp[j + half] = sn;
+}
+
+// ---------------------------------------------------------------------------------------
+// apply_rotary: out = x*cos + rotate_half(x)*sin; one thread owns VEC features of the first
+// half and the matching VEC features of the second half of one (b, s, h) row.
+// ---------------------------------------------------------------------------------------
+template <typename T, typename M, int VEC>
+__device__ __forceinline__ void rotate_pair(const T (&x1)[VEC], const T (&x2)[VEC],
+                                            const T (&c1)[VEC], const T (&c2)[VEC],
+                                            const T (&s1)[VEC], const T (&s2)[VEC],
+                                            T (&o1)[VEC], T (&o2)[VEC]) {
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    const M a1 = widen<T, M>(x1[e]), a2 = widen<T, M>(x2[e]);
+    // first half: x1*cos + (-x2)*sin ; second half: x2*cos + x1*sin
+    const M p1 = rnd<T, M>(mul_rn(a1, widen<T, M>(c1[e])));
+    const M q1 = rnd<T, M>(mul_rn(-a2, widen<T, M>(s1[e])));
+    const M p2 = rnd<T, M>(mul_rn(a2, widen<T, M>(c2[e])));
+    const M q2 = rnd<T, M>(mul_rn(a1, widen<T, M>(s2[e])));
+    o1[e] = narrow<T, M>(add_rn(p1, q1));
+    o2[e] = narrow<T, M>(add_rn(p2, q2));
+  }
+}
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void apply_rotary_kernel(
+    const T* __restrict__ x, int64_t xs_b, int64_t xs_s, int64_t xs_h,
+    const T* __restrict__ cosb, int64_t cs_b, int64_t cs_s, const T* __restrict__ sinb,
+    int64_t ss_b, int64_t ss_s, T* __restrict__ out, int64_t os_b, int64_t os_s, int64_t os_h,
+    int B, int S, int H, int D) {
+  typedef typename math_of<T>::type M;
+  const int half = D / 2;
+  const int nch = half / VEC;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)B * S * H * nch;
+  if (t >= total) return;
+  const int j = (int)(t % nch) * VEC;
+  int64_t r = t / nch;
+  const int h = (int)(r % H);
+  r /= H;
+  const int s = (int)(r % S);
+  const int b = (int)(r / S);
+  const T* xr = x + b * xs_b + s * xs_s + h * xs_h;
+  const T* cr = cosb + b * cs_b + s * cs_s;
+  const T* sr = sinb + b * ss_b + s * ss_s;
+  T x1[VEC], x2[VEC], c1[VEC], c2[VEC], s1[VEC], s2[VEC], o1[VEC], o2[VEC];
+  load_vec<T, VEC>(xr + j, x1);
+  load_vec<T, VEC>(xr + j + half, x2);
+  load_vec<T, VEC>(cr + j, c1);
+  load_vec<T, VEC>(cr + j + half, c2);
+  load_vec<T, VEC>(sr + j, s1);
+  load_vec<T, VEC>(sr + j + half, s2);
+  rotate_pair<T, M, VEC>(x1, x2, c1, c2, s1, s2, o1, o2);
+  T* orow = out + b * os_b + s * os_s + h * os_h;
+  store_vec<T, VEC>(orow + j, o1);
+  store_vec<T, VEC>(orow + j + half, o2);
+}
+
+// ---------------------------------------------------------------------------------------
+// fused RMSNorm + rotary: one 256-thread block per token row of H*D features.  The row's
+// rotary tables (D/2 angles) are evaluated once into LDS; every feature pair (j, j+D/2) of
+// every head is normalised, weighted and rotated in registers.
+// ---------------------------------------------------------------------------------------
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void rmsnorm_rope_kernel(
+    const T* __restrict__ x, int64_t xs, const T* __restrict__ w, const int64_t* __restrict__ pos,
+    int64_t ps, const typename math_of<T>::type* __restrict__ inv_freq, T* __restrict__ out,
+    int64_t os, int H, int D, double eps_d) {
+  typedef typename math_of<T>::type M;
+  __shared__ M red[4];
+  __shared__ T tab_c[512];
+  __shared__ T tab_s[512];
+  const int64_t row = blockIdx.x;
+  const int C = H * D;
+  const int half = D / 2;
+  const T* xr = x + row * xs;
+  T* orow = out + row * os;
+
+  M ss = 0;
+  for (int c = threadIdx.x * VEC; c < C; c += 256 * VEC) {
+    T v[VEC];
+    load_vec<T, VEC>(xr + c, v);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const M h = widen<T, M>(v[e]);
+      ss += h * h;
+    }
+  }
+  const M pf = pos_to<M>(pos[row * ps]);
+  for (int j = threadIdx.x; j < half; j += 256) {
+    M sv, cv;
+    sincos_acc(mul_rn(pf, inv_freq[j]), &sv, &cv);
+    tab_c[j] = narrow<T, M>(cv);
+    tab_s[j] = narrow<T, M>(sv);
+  }
+  ss = block_sum_256<M>(ss, red);  // contains the barrier that publishes the tables
+  const M r = rsqrt_rn(add_rn(div_rn(ss, (M)C), (M)eps_d));
+
+  const int nch = half / VEC;
+  for (int it = threadIdx.x; it < H * nch; it += 256) {
+    const int h = it / nch;
+    const int j = (it % nch) * VEC;
+    const int c1 = h * D + j, c2 = c1 + half;
+    T x1[VEC], x2[VEC], w1[VEC], w2[VEC], y1[VEC], y2[VEC], cs[VEC], sn[VEC], o1[VEC], o2[VEC];
+    load_vec<T, VEC>(xr + c1, x1);
+    load_vec<T, VEC>(xr + c2, x2);
+    load_vec<T, VEC>(w + c1, w1);
+    load_vec<T, VEC>(w + c2, w2);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      y1[e] = narrow<T, M>(mul_rn(widen<T, M>(w1[e]),
+                                  rnd<T, M>(mul_rn(widen<T, M>(x1[e]), r))));
+      y2[e] = narrow<T, M>(mul_rn(widen<T, M>(w2[e]),
+                                  rnd<T, M>(mul_rn(widen<T, M>(x2[e]), r))));
+      cs[e] = tab_c[j + e];
+      sn[e] = tab_s[j + e];
+    }
+    rotate_pair<T, M, VEC>(y1, y2, cs, cs, sn, sn, o1, o2);
+    store_vec<T, VEC>(orow + c1, o1);
+    store_vec<T, VEC>(orow + c2, o2);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// SiLU-gate: out = silu(gate) * up with silu(g) = g / (1 + exp(-g)) rounded to T first.
+// ---------------------------------------------------------------------------------------
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ g, int64_t gs,
+                                                       const T* __restrict__ u, int64_t us,
+                                                       T* __restrict__ out, int64_t os,
+                                                       int64_t N, int I) {
+  typedef typename math_of<T>::type M;
+  const int nch = I / VEC;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * nch) return;
+  const int64_t row = t / nch;
+  const int c = (int)(t % nch) * VEC;
+  T gv[VEC], uv[VEC], ov[VEC];
+  load_vec<T, VEC>(g + row * gs + c, gv);
+  load_vec<T, VEC>(u + row * us + c, uv);
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    const M a = widen<T, M>(gv[e]);
+    const M sl = rnd<T, M>(div_rn(a, add_rn((M)1, exp_acc(-a))));
+    ov[e] = narrow<T, M>(mul_rn(sl, widen<T, M>(uv[e])));
+  }
+  store_vec<T, VEC>(out + row * os + c, ov);
+}
+
+// ---------------------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------------------
+static bool al(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+static bool strides_ok(std::initializer_list<int64_t> s, size_t esz, size_t a) {
+  for (int64_t v : s)
+    if (((uint64_t)v * esz) % a) return false;
+  return true;
+}
+
+template <typename T, typename W, typename O>
+static int rmsnorm_typed(const cea_tensor* x, const cea_tensor* w, double eps, cea_tensor* y,
+                         hipStream_t st) {
+  const int64_t N = x->size[0];
+  const int C = (int)x->size[1];
+  if (N == 0 || C == 0) return CEA_OK;
+  constexpr int VEC = 16 / sizeof(T) < 16 / sizeof(W) ? 16 / sizeof(T) : 16 / sizeof(W);
+  const bool vec = C % VEC == 0 && al(x->data, 16) && al(w->data, 16) &&
+                   al(y->data, VEC * sizeof(O)) && strides_ok({x->stride[0]}, sizeof(T), 16) &&
+                   strides_ok({y->stride[0]}, sizeof(O), VEC * sizeof(O));
+  CEA_REQUIRE(N < (int64_t)1 << 31, CEA_EUNSUPPORTED, "rmsnorm: too many rows");
+  if (vec)
+    hipLaunchKernelGGL((rmsnorm_kernel<T, W, O, VEC, 4>), dim3(N), dim3(256), 0, st,
+                       (const T*)x->data, x->stride[0], (const W*)w->data, (O*)y->data,
+                       y->stride[0], C, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<T, W, O, 1, 8>), dim3(N), dim3(256), 0, st,
+                       (const T*)x->data, x->stride[0], (const W*)w->data, (O*)y->data,
+                       y->stride[0], C, eps);
+  CEA_CHECK_LAUNCH("rmsnorm");
+  return CEA_OK;
+}
+
+int launch_rmsnorm(const cea_tensor* x, const cea_tensor* w, double eps, cea_tensor* y,
+                   hipStream_t st) {
+  const int xt = x->dtype, wt = w->dtype, yt = y->dtype;
+  if (xt == CEA_BF16 && wt == CEA_BF16 && yt == CEA_BF16) return rmsnorm_typed<bf16, bf16, bf16>(x, w, eps, y, st);
+  if (xt == CEA_F16 && wt == CEA_F16 && yt == CEA_F16) return rmsnorm_typed<f16, f16, f16>(x, w, eps, y, st);
+  if (xt == CEA_F32 && wt == CEA_F32 && yt == CEA_F32) return rmsnorm_typed<float, float, float>(x, w, eps, y, st);
+  if (xt == CEA_F64 && wt == CEA_F64 && yt == CEA_F64) return rmsnorm_typed<double, double, double>(x, w, eps, y, st);
+  if (xt == CEA_BF16 && wt == CEA_F32 && yt == CEA_F32) return rmsnorm_typed<bf16, float, float>(x, w, eps, y, st);
+  if (xt == CEA_F16 && wt == CEA_F32 && yt == CEA_F32) return rmsnorm_typed<f16, float, float>(x, w, eps, y, st);
+  set_error("rmsnorm: unsupported dtype combination x=%s weight=%s y=%s", dtype_name(xt),
+            dtype_name(wt), dtype_name(yt));
+  return CEA_EUNSUPPORTED;
+}
+
+template <typename T>
+static int rope_tables_typed(const cea_tensor* pos, const cea_tensor* inv, cea_tensor* c,
+                             cea_tensor* s, hipStream_t st) {
+  const int B = (int)pos->size[0], S = (int)pos->size[1];
+  const int half = (int)inv->size[0];
+  const int64_t total = (int64_t)B * S * half;
+  if (total == 0) return CEA_OK;
+  const int64_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL((rope_tables_kernel<T>), dim3(blocks), dim3(256), 0, st,
+                     (const int64_t*)pos->data, pos->stride[0], pos->stride[1],
+                     (const typename math_of<T>::type*)inv->data, (T*)c->data, (T*)s->data,
+                     c->stride[0], c->stride[1], s->stride[0], s->stride[1], B, S, half);
+  CEA_CHECK_LAUNCH("rope_tables");
+  return CEA_OK;
+}
+
+int launch_rope_tables(const cea_tensor* pos, const cea_tensor* inv, cea_tensor* c,
+                       cea_tensor* s, hipStream_t st) {
+  switch (c->dtype) {
+    case CEA_BF16: return rope_tables_typed<bf16>(pos, inv, c, s, st);
+    case CEA_F16: return rope_tables_typed<f16>(pos, inv, c, s, st);
+    case CEA_F32: return rope_tables_typed<float>(pos, inv, c, s, st);
+    case CEA_F64: return rope_tables_typed<double>(pos, inv, c, s, st);
+  }
+  set_error("rope_tables: unsupported table dtype %s", dtype_name(c->dtype));
+  return CEA_EUNSUPPORTED;
+}
+
+template <typename T>
+static int apply_rotary_typed(const cea_tensor* x, const cea_tensor* c, const cea_tensor* s,
+                              cea_tensor* o, hipStream_t st) {
+  const int B = (int)x->size[0], S = (int)x->size[1], H = (int)x->size[2], D = (int)x->size[3];
+  const int half = D / 2;
+  constexpr int V = 16 / sizeof(T);
+  const bool vec = half % V == 0 && al(x->data, 16) && al(c->data, 16) && al(s->data, 16) &&
+                   al(o->data, 16) &&
+                   strides_ok({x->stride[0], x->stride[1], x->stride[2], c->stride[0],
+                               c->stride[1], s->stride[0], s->stride[1], o->stride[0],
+                               o->stride[1], o->stride[2], (int64_t)half},
+                              sizeof(T), 16);
+  const int vecw = vec ? V : 1;
+  const int64_t total = (int64_t)B * S * H * (half / vecw);
+  if (total == 0) return CEA_OK;
+  const int64_t blocks = (total + 255) / 256;
+#define CEA_ROT_ARGS                                                                      \
+  (const T*)x->data, x->stride[0], x->stride[1], x->stride[2], (const T*)c->data,         \
+      c->stride[0], c->stride[1], (const T*)s->data, s->stride[0], s->stride[1],         \
+      (T*)o->data, o->stride[0], o->stride[1], o->stride[2], B, S, H, D
+  if (vec)
+    hipLaunchKernelGGL((apply_rotary_kernel<T, V>), dim3(blocks), dim3(256), 0, st, CEA_ROT_ARGS);
+  else
+    hipLaunchKernelGGL((apply_rotary_kernel<T, 1>), dim3(blocks), dim3(256), 0, st, CEA_ROT_ARGS);
+#undef CEA_ROT_ARGS
+  CEA_CHECK_LAUNCH("apply_rotary");
+  return CEA_OK;
+}
+
+int launch_apply_rotary(const cea_tensor* x, const cea_tensor* c, const cea_tensor* s,
+                        cea_tensor* o, hipStream_t st) {
+  switch (x->dtype) {
+    case CEA_BF16: return apply_rotary_typed<bf16>(x, c, s, o, st);
+    case CEA_F16: return apply_rotary_typed<f16>(x, c, s, o, st);
+    case CEA_F32: return apply_rotary_typed<float>(x, c, s, o, st);
+    case CEA_F64: return apply_rotary_typed<double>(x, c, s, o, st);
+  }
+  set_error("apply_rotary: unsupported dtype %s", dtype_name(x->dtype));
+  return CEA_EUNSUPPORTED;
+}
+
+template <typename T>
+static int rmsnorm_rope_typed(const cea_tensor* x, const cea_tensor* w, double eps,
+                              const cea_tensor* pos, const cea_tensor* inv, int H,
+                              cea_tensor* o, hipStream_t st) {
+  const int64_t S = x->size[0];
+  const int C = (int)x->size[1];
+  const int D = C / H, half = D / 2;
+  if (S == 0) return CEA_OK;
+  constexpr int V = 16 / sizeof(T);
+  const bool vec = half % V == 0 && al(x->data, 16) && al(w->data, 16) && al(o->data, 16) &&
+                   strides_ok({x->stride[0], o->stride[0], (int64_t)half}, sizeof(T), 16);
+  const int64_t ps = pos->ndim == 2 ? pos->stride[1] : pos->stride[0];
+#define CEA_RR_ARGS                                                                    \
+  (const T*)x->data, x->stride[0], (const T*)w->data, (const int64_t*)pos->data, ps,   \
+      (const typename math_of<T>::type*)inv->data, (T*)o->data, o->stride[0], H, D, eps
+  if (vec)
+    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, V>), dim3(S), dim3(256), 0, st, CEA_RR_ARGS);
+  else
+    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 1>), dim3(S), dim3(256), 0, st, CEA_RR_ARGS);
+#undef CEA_RR_ARGS
+  CEA_CHECK_LAUNCH("rmsnorm_rope");
+  return CEA_OK;
+}
+
+int launch_rmsnorm_rope(const cea_tensor* x, const cea_tensor* w, double eps,
+                        const cea_tensor* pos, const cea_tensor* inv, int H, cea_tensor* o,
+                        hipStream_t st) {
+  switch (x->dtype) {
+    case CEA_BF16: return rmsnorm_rope_typed<bf16>(x, w, eps, pos, inv, H, o, st);
+    case CEA_F16: return rmsnorm_rope_typed<f16>(x, w, eps, pos, inv, H, o, st);
+    case CEA_F32: return rmsnorm_rope_typed<float>(x, w, eps, pos, inv, H, o, st);
+    case CEA_F64: return rmsnorm_rope_typed<double>(x, w, eps, pos, inv, H, o, st);
+  }
+  set_error("rmsnorm_rope: unsupported dtype %s", dtype_name(x->dtype));
+  return CEA_EUNSUPPORTED;
+}
+
+template <typename T>
+static int silu_mul_typed(const cea_tensor* g, const cea_tensor* u, cea_tensor* o,
+                          hipStream_t st) {
+  const int64_t N = g->size[0];
+  const int I = (int)g->size[1];
+  constexpr int V = 16 / sizeof(T);
+  const bool vec = I % V == 0 && al(g->data, 16) && al(u->data, 16) && al(o->data, 16) &&
+                   strides_ok({g->stride[0], u->stride[0], o->stride[0]}, sizeof(T), 16);
+  const int vw = vec ? V : 1;
+  const int64_t total = N * (I / vw);
+  if (total == 0) return CEA_OK;
+  const int64_t blocks = (total + 255) / 256;
+  if (vec)
+    hipLaunchKernelGGL((silu_mul_kernel<T, V>), dim3(blocks), dim3(256), 0, st,
+                       (const T*)g->data, g->stride[0], (const T*)u->data, u->stride[0],
+                       (T*)o->data, o->stride[0], N, I);
+  else
+    hipLaunchKernelGGL((silu_mul_kernel<T, 1>), dim3(blocks), dim3(256), 0, st,
+                       (const T*)g->data, g->stride[0], (const T*)u->data, u->stride[0],
+                       (T*)o->data, o->stride[0], N, I);
+  CEA_CHECK_LAUNCH("silu_mul");
+  return CEA_OK;
+}
+
+int launch_silu_mul(const cea_tensor* g, const cea_tensor* u, cea_tensor* o, hipStream_t st) {
+  switch (g->dtype) {
+    case CEA_BF16: return silu_mul_typed<bf16>(g, u, o, st);
+    case CEA_F16: return silu_mul_typed<f16>(g, u, o, st);
+    case CEA_F32: return silu_mul_typed<float>(g, u, o, st);
+    case CEA_F64: return silu_mul_typed<double>(g, u, o, st);
+  }
+  set_error("silu_mul: unsupported dtype %s", dtype_name(g->dtype));
+  return CEA_EUNSUPPORTED;
+}
+
+}  // namespace cea

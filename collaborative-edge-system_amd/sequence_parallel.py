@@ -1,0 +1,369 @@
+"""One rank's share of ring attention, Ulysses attention and distributed-KV decoding, run on
+one GPU.
+
+Drop-in signatures of collab_infer/parallel/sequence_parallel.py.  The collectives are not
+part of this build: the ``comm`` argument is a :class:`LocalGroup` that already holds what
+the other simulated ranks would send (their KV blocks, partitions or token shards), so a
+rank's share is computed at its real shape by streaming those blocks through the kernels:
+
+* :func:`ring_attention` (sequence_parallel.py:68-130) - the rank's queries against every
+  rank's KV block in ring order ``(r - step) mod n``, each block merged exactly into a
+  running ``(out, lse)`` in the attention kernel's epilogue.  Fully hidden blocks cost one
+  pass over their position summaries (the kernel skips their tiles), which replaces the
+  reference's host-side ``fully_masked`` test without a device-to-host sync.
+* :func:`distributed_kv_attention` (sequence_parallel.py:250-280) - a replicated query
+  against every rank's cache partition, partials merged exactly (``merge_attention_list``).
+* :func:`ulysses_scatter` / :func:`ulysses_gather` / :func:`ulysses_attention`
+  (sequence_parallel.py:143-239) - the all-to-all data movement as concatenation, then the
+  head-sharded local attention over the full sequence.
+
+A group of size 1 is the single-device case of the reference (its ``n == 1`` branches).
+"""
+
+from __future__ import annotations
+
+from ctypes import byref
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _native as nat
+from .attention import (
+    KVMap,
+    _kv_map_list,
+    _check_heads,
+    _inner_contiguous,
+    _positions,
+    accumulation_dtype,
+    attention,
+    attention_with_lse,
+    attention_with_lse_into,
+    merge_attention_list,
+)
+from .partition import HeadShard, SequenceLayout, offsets_of
+
+import math
+
+
+class LocalGroup:
+    """A group of ``size`` simulated ranks on one GPU, seen from rank ``rank``.
+
+    It stands in for collab_infer's ``Communicator`` (distributed/comm.py:200): instead of
+    exchanging messages, every rank's shard is registered up front with :meth:`set_shard`
+    (keys ``k``, ``v``, ``pos`` for KV blocks; ``q`` too for Ulysses).  ``wire_dtype``
+    mirrors the ring's wire compression (``Communicator.to_wire``, comm.py:275-290): blocks
+    received from other ranks are rounded through that dtype.
+    """
+
+    def __init__(self, size: int, rank: int = 0, wire_dtype: Optional[torch.dtype] = None) -> None:
+        if size < 1 or not 0 <= rank < size:
+            raise ValueError(f"invalid rank {rank} for a group of {size}")
+        self.size = int(size)
+        self.rank = int(rank)
+        self.wire_dtype = wire_dtype
+        self._shards: Dict[int, Dict[str, torch.Tensor]] = {}
+
+    def set_shard(self, rank: int, **tensors: torch.Tensor) -> "LocalGroup":
+        self._shards.setdefault(int(rank), {}).update(tensors)
+        return self
+
+    def shard(self, rank: int) -> Dict[str, torch.Tensor]:
+        if rank not in self._shards:
+            raise RuntimeError(f"no data registered for simulated rank {rank}")
+        return self._shards[rank]
+
+    def view_as(self, rank: int) -> "LocalGroup":
+        """The same group seen from another rank (shares the registered shards)."""
+        g = LocalGroup(self.size, rank, self.wire_dtype)
+        g._shards = self._shards
+        return g
+
+    def received(self, t: torch.Tensor) -> torch.Tensor:
+        if self.wire_dtype is None or self.wire_dtype == t.dtype:
+            return t
+        return t.to(self.wire_dtype).to(t.dtype)
+
+
+def _kv_from(comm: LocalGroup, src: int, own: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]):
+    if src == comm.rank:
+        return own
+    s = comm.shard(src)
+    return comm.received(s["k"]), comm.received(s["v"]), s["pos"]
+
+
+# --------------------------------------------------------------------------------------
+# ring attention
+# --------------------------------------------------------------------------------------
+def ring_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_pos: torch.Tensor,
+    k_pos: torch.Tensor,
+    comm: LocalGroup,
+    kv_sizes: Sequence[int],
+    *,
+    causal: bool = True,
+    scale: Optional[float] = None,
+    kv_map: KVMap = None,
+    kv_block: Optional[int] = None,
+) -> torch.Tensor:
+    """Attention of this rank's queries over the KV blocks of all ranks
+    (sequence_parallel.py:68-130); returns ``[B, s_r, Hq, D]`` in ``q.dtype``."""
+    out, _ = ring_attention_with_lse(q, k, v, q_pos, k_pos, comm, kv_sizes, causal=causal,
+                                     scale=scale, kv_map=kv_map, kv_block=kv_block)
+    return out.to(q.dtype)
+
+
+def ring_attention_with_lse(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_pos: torch.Tensor,
+    k_pos: torch.Tensor,
+    comm: LocalGroup,
+    kv_sizes: Sequence[int],
+    *,
+    causal: bool = True,
+    scale: Optional[float] = None,
+    kv_map: KVMap = None,
+    kv_block: Optional[int] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """:func:`ring_attention` returning the merged ``(out, lse)`` in accumulation precision."""
+    n, r = comm.size, comm.rank
+    if n == 1:
+        return attention_with_lse(q, k, v, q_pos, k_pos, causal=causal, scale=scale,
+                                  kv_map=kv_map, kv_block=kv_block)
+    if len(kv_sizes) != n or kv_sizes[r] != k.shape[1]:
+        raise ValueError(f"kv_sizes {list(kv_sizes)} inconsistent with local block of {k.shape[1]} tokens")
+    B, Sq, Hq, D = q.shape
+    acc = accumulation_dtype(q.dtype)
+    out = torch.zeros(B, Sq, Hq, D, dtype=acc, device=q.device)
+    lse = torch.full((B, Hq, Sq), float("-inf"), dtype=acc, device=q.device)
+    own = (k, v, k_pos)
+    for step in range(n):
+        kb, vb, pb = _kv_from(comm, (r - step) % n, own)
+        if kb.shape[1] != kv_sizes[(r - step) % n]:
+            raise ValueError(f"kv_sizes {list(kv_sizes)} inconsistent with the block of rank {(r - step) % n}")
+        blk = kv_block if kv_block is not None and kv_block < kb.shape[1] else kb.shape[1]
+        for start in range(0, kb.shape[1], max(1, blk)):
+            end = min(start + blk, kb.shape[1])
+            attention_with_lse_into(out, lse, q, kb[:, start:end], vb[:, start:end], q_pos,
+                                    pb[:, start:end], causal=causal, scale=scale, kv_map=kv_map)
+    return out, lse
+
+
+# --------------------------------------------------------------------------------------
+# distributed-KV decoding
+# --------------------------------------------------------------------------------------
+def partitioned_attention(
+    q: torch.Tensor,
+    q_pos: torch.Tensor,
+    parts: Sequence[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
+    *,
+    causal: bool = True,
+    scale: Optional[float] = None,
+    kv_map: KVMap = None,
+    out_dtype: Optional[torch.dtype] = None,
+    return_lse: bool = False,
+    return_parts: bool = False,
+):
+    """Attention of ``q`` against KV partitions ``[(k_p, v_p, pos_p), ...]`` plus the exact
+    merge, in the kernels of ``cea_partitioned_attention``.
+
+    Returns ``out`` (``out_dtype``, default ``q.dtype``), plus ``lse`` and the list of
+    per-partition ``(out_p, lse_p)`` (each rank's ``attention_with_lse``) when asked.
+    """
+    parts = list(parts)
+    if not parts:
+        raise ValueError("need at least one partition")
+    if len(parts) > nat.MAX_PARTS:
+        raise NotImplementedError(f"at most {nat.MAX_PARTS} partitions per call")
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
+    nat.require_device(q, q_pos, *[t for p in parts for t in p])
+    mapping = _kv_map_list(kv_map)
+    q = _inner_contiguous(q)
+    q_pos = _positions(q_pos)
+    ks = [_inner_contiguous(p[0]) for p in parts]
+    vs = [_inner_contiguous(p[1]) for p in parts]
+    ps = [_positions(p[2]) for p in parts]
+    for kk in ks:
+        _check_heads(q.shape[2], kk.shape[2], mapping)
+    B, Sq, Hq, D = q.shape
+    acc = accumulation_dtype(q.dtype)
+    out = torch.empty(B, Sq, Hq, D, dtype=out_dtype or q.dtype, device=q.device)
+    lse = torch.empty(B, Hq, Sq, dtype=acc, device=q.device) if return_lse else None
+    lib = nat.load_library()
+    n = len(parts)
+    part_out = part_lse = None
+    if return_parts:
+        part_out = [torch.empty(B, Sq, Hq, D, dtype=acc, device=q.device) for _ in range(n)]
+        part_lse = [torch.empty(B, Hq, Sq, dtype=acc, device=q.device) for _ in range(n)]
+    import ctypes
+
+    sks = (ctypes.c_int64 * n)(*[kk.shape[1] for kk in ks])
+    ws_bytes = lib.cea_partitioned_attention_workspace_bytes(
+        n, sks, B, Sq, Hq, ks[0].shape[2], D, nat.DTYPE_CODES[q.dtype])
+    ws = nat.workspace(ws_bytes, q.device)
+    km, kn = nat.kv_map_arg(mapping)
+    qa, qpa = nat.tensor_arg(q), nat.tensor_arg(q_pos)
+    ka, va, pa = nat.tensor_array(ks), nat.tensor_array(vs), nat.tensor_array(ps)
+    oa = nat.tensor_arg(out)
+    la = nat.tensor_arg(lse) if lse is not None else None
+    poa = nat.tensor_array(part_out) if part_out else None
+    pla = nat.tensor_array(part_lse) if part_lse else None
+    rc = lib.cea_partitioned_attention(
+        byref(qa), n, ka, va, byref(qpa), pa, int(bool(causal)), float(scale), km, kn, poa, pla,
+        byref(oa), byref(la) if la is not None else None, ws.data_ptr(), ws.numel(),
+        nat.stream_of(q.device))
+    nat.check(rc, "partitioned_attention")
+    result = [out]
+    if return_lse:
+        result.append(lse)
+    if return_parts:
+        result.append(list(zip(part_out, part_lse)))
+    return result[0] if len(result) == 1 else tuple(result)
+
+
+def distributed_kv_attention(
+    q: torch.Tensor,
+    k_local: torch.Tensor,
+    v_local: torch.Tensor,
+    q_pos: torch.Tensor,
+    k_pos_local: torch.Tensor,
+    comm: LocalGroup,
+    *,
+    causal: bool = True,
+    scale: Optional[float] = None,
+    kv_map: KVMap = None,
+    kv_block: Optional[int] = None,
+) -> torch.Tensor:
+    """A replicated query against a KV cache sharded over the ranks of ``comm``
+    (sequence_parallel.py:250-280); returns ``[B, Sq, Hq, D]`` in ``q.dtype``."""
+    if comm.size == 1:
+        o, _ = attention_with_lse(q, k_local, v_local, q_pos, k_pos_local, causal=causal,
+                                  scale=scale, kv_map=kv_map, kv_block=kv_block)
+        return o.to(q.dtype)
+    own = (k_local, v_local, k_pos_local)
+    parts = [_kv_from(comm, i, own) for i in range(comm.size)]  # rank order, as all_gather
+    if kv_block is not None:
+        partial = [attention_with_lse(q, kk, vv, q_pos, pp, causal=causal, scale=scale,
+                                      kv_map=kv_map, kv_block=kv_block) for kk, vv, pp in parts]
+        o, _ = merge_attention_list([p[0] for p in partial], [p[1] for p in partial])
+        return o.to(q.dtype)
+    return partitioned_attention(q, q_pos, parts, causal=causal, scale=scale, kv_map=kv_map)
+
+
+# --------------------------------------------------------------------------------------
+# Ulysses
+# --------------------------------------------------------------------------------------
+def _check_ulysses(comm: LocalGroup, seq_sizes: Sequence[int], head_shards: Sequence[HeadShard],
+                   s_local: int) -> None:
+    if len(seq_sizes) != comm.size or seq_sizes[comm.rank] != s_local:
+        raise ValueError(f"seq_sizes {list(seq_sizes)} inconsistent with local shard of {s_local} tokens")
+    if len(head_shards) != comm.size:
+        raise ValueError("need one head shard per rank")
+
+
+def ulysses_scatter(q, k, v, positions, comm: LocalGroup, seq_sizes: Sequence[int],
+                    head_shards: Sequence[HeadShard]):
+    """Sequence-sharded -> head-sharded (sequence_parallel.py:143-179): this rank's heads over
+    the whole sequence, tokens concatenated in rank order, with their positions ``[B, S]``."""
+    n, r = comm.size, comm.rank
+    _check_ulysses(comm, seq_sizes, head_shards, q.shape[1])
+    me = head_shards[r]
+    qs, ks, vs, ps = [], [], [], []
+    for j in range(n):
+        if j == r:
+            sq, sk, sv, sp = q, k, v, positions
+        else:
+            s = comm.shard(j)
+            sq, sk, sv, sp = s["q"], s["k"], s["v"], s["pos"]
+            if sq.shape[1] != seq_sizes[j]:
+                raise ValueError(f"seq_sizes {list(seq_sizes)} inconsistent with rank {j}")
+        qs.append(sq[:, :, me.q_start : me.q_start + me.q_count])
+        ks.append(sk[:, :, me.kv_start : me.kv_start + me.kv_count])
+        vs.append(sv[:, :, me.kv_start : me.kv_start + me.kv_count])
+        ps.append(sp)
+    cat = (lambda xs: torch.cat(xs, dim=1)) if n > 1 else (lambda xs: xs[0])
+    return cat(qs), cat(ks), cat(vs), cat(ps)
+
+
+def ulysses_gather(out_heads_of_ranks: Sequence[torch.Tensor], comm: LocalGroup,
+                   seq_sizes: Sequence[int], head_shards: Sequence[HeadShard]) -> torch.Tensor:
+    """Head-sharded -> sequence-sharded (sequence_parallel.py:182-194).  On one GPU every
+    rank's head output ``[B, S, h_j, D]`` is available; returns this rank's tokens with all
+    heads ``[B, s_r, H, D]``."""
+    r = comm.rank
+    start = offsets_of(seq_sizes)[r]
+    pieces = [o[:, start : start + seq_sizes[r]] for o in out_heads_of_ranks]
+    return torch.cat(pieces, dim=2) if len(pieces) > 1 else pieces[0]
+
+
+def ulysses_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    positions: torch.Tensor,
+    comm: LocalGroup,
+    seq_sizes: Sequence[int],
+    head_shards: Sequence[HeadShard],
+    *,
+    causal: bool = True,
+    scale: Optional[float] = None,
+    past: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None,
+    kv_block: Optional[int] = None,
+):
+    """All-to-all sequence-parallel attention (sequence_parallel.py:197-239).
+
+    Every simulated rank's head-sharded local attention runs here (the gather needs all of
+    them); returns ``(out [B, s_r, Hq, D], (k_heads, v_heads, pos_full))`` for this rank.
+    """
+    outs = []
+    mine = None
+    for j in range(comm.size):
+        cj = comm.view_as(j)
+        if j == comm.rank:
+            sq, sk, sv, sp = q, k, v, positions
+        else:
+            s = comm.shard(j)
+            sq, sk, sv, sp = s["q"], s["k"], s["v"], s["pos"]
+        q_f, k_f, v_f, pos_f = ulysses_scatter(sq, sk, sv, sp, cj, seq_sizes, head_shards)
+        k_att, v_att, p_att = k_f, v_f, pos_f
+        if j == comm.rank and past is not None and past[0].shape[1] > 0:
+            k_att = torch.cat([past[0], k_f], dim=1)
+            v_att = torch.cat([past[1], v_f], dim=1)
+            p_att = torch.cat([past[2], pos_f], dim=1)
+        elif j != comm.rank and "past" in comm.shard(j) and comm.shard(j)["past"][0].shape[1] > 0:
+            pk, pv, pp = comm.shard(j)["past"]
+            k_att, v_att, p_att = (torch.cat([pk, k_f], 1), torch.cat([pv, v_f], 1),
+                                   torch.cat([pp, pos_f], 1))
+        outs.append(attention(q_f, k_att, v_att, pos_f, p_att, causal=causal, scale=scale,
+                              kv_map=head_shards[j].kv_map, kv_block=kv_block))
+        if j == comm.rank:
+            mine = (k_f.contiguous(), v_f.contiguous(), pos_f)
+    return ulysses_gather(outs, comm, seq_sizes, head_shards), mine
+
+
+def gather_sequence(x_parts: Sequence[torch.Tensor], layout: SequenceLayout, dim: int = 1) -> torch.Tensor:
+    """Reassemble per-rank sequence shards in global token order (sequence_parallel.py:55-62)."""
+    return layout.unshard(list(x_parts), dim=dim)
+
+
+def shard_sequence(x: torch.Tensor, layout: SequenceLayout, rank: int, dim: int = 1) -> torch.Tensor:
+    """This rank's tokens of a full-sequence tensor (sequence_parallel.py:50-52)."""
+    return layout.shard(x, rank, dim)
+
+
+__all__ = [
+    "LocalGroup",
+    "distributed_kv_attention",
+    "gather_sequence",
+    "partitioned_attention",
+    "ring_attention",
+    "ring_attention_with_lse",
+    "shard_sequence",
+    "ulysses_attention",
+    "ulysses_gather",
+    "ulysses_scatter",
+]

@@ -1,0 +1,259 @@
+"""Seeded synthetic inputs of the five workloads of the attention / layer-op path, and their
+algorithmic work counts.
+
+Inputs are drawn on the CPU from ``torch.Generator().manual_seed(seed)`` in f32 (as the
+reference's tests do, tests/test_sequence_parallel.py:18-22), then cast and moved, so the
+CPU oracle and the GPU see bit-identical inputs.
+
+* ``attn_f32_split``   - f32 attention B=1, 8/8 heads, S=512, D=64, causal, plus a 2-way KV
+  split merged by LSE.
+* ``layer_ops``        - bf16 RMSNorm + rotary on a 4096 x 4096 activation viewed as
+  32 heads x 128 (theta 1e4, positions 0..4095) and SiLU-gate on 4096 x 14336 gate/up.
+* ``ring_share``       - rank 0 of a 4-rank zigzag ring over 32768 tokens: 8192 local queries
+  (positions 0..4095 and 28672..32767), 32/8 GQA heads, D=128, bf16; four 8192-token KV
+  blocks streamed in ring order 0, 3, 2, 1 (sequence_parallel.py:107-110).
+* ``kv_decode``        - distributed-KV decode: B=32, one query token, 32/8 heads, D=128,
+  bf16; head-major cache ``[32, 8, 32768, 128]`` (models/cache.py:11-20) with valid lengths
+  uniform in [1024, 32768]; four contiguous partitions with weights 0.4/0.3/0.2/0.1.
+* ``ulysses_share``    - rank 0 of an 8-way Ulysses split of a 64/16-head model: 65536 tokens,
+  8/2 heads, D=128, bf16, causal, 4 packed sequences followed by right padding.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from .partition import SequenceLayout, partition_heads, split_sizes
+
+
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(int(seed))
+
+
+def _randn(g: torch.Generator, *shape, dtype=torch.bfloat16, device="cpu") -> torch.Tensor:
+    return torch.randn(*shape, generator=g, dtype=torch.float32).to(dtype).to(device)
+
+
+def visible_pairs(q_pos: torch.Tensor, k_pos: torch.Tensor, causal: bool = True) -> int:
+    """Exact number of visible (query, key) pairs for one head of a ``[1, S]`` position pair."""
+    kp = k_pos.reshape(-1).to(torch.int64).cpu()
+    kp = torch.sort(kp[kp >= 0]).values
+    qp = q_pos.reshape(-1).to(torch.int64).cpu()
+    if not causal:
+        return int(kp.numel()) * int(qp.numel())
+    return int(torch.searchsorted(kp, qp, right=True).sum())
+
+
+# --------------------------------------------------------------------------------------
+@dataclass
+class AttnF32Split:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    pos: torch.Tensor
+    scale: float
+    split: int
+    flop: int
+
+
+def attn_f32_split(device="cpu", seed: int = 0) -> AttnF32Split:
+    g = _gen(seed)
+    B, H, S, D = 1, 8, 512, 64
+    q = _randn(g, B, S, H, D, dtype=torch.float32, device=device)
+    k = _randn(g, B, S, H, D, dtype=torch.float32, device=device)
+    v = _randn(g, B, S, H, D, dtype=torch.float32, device=device)
+    pos = torch.arange(S, device=device).view(1, S)
+    flop = 4 * D * H * S * (S + 1) // 2
+    return AttnF32Split(q, k, v, pos, 1.0 / 8.0, 256, flop)
+
+
+# --------------------------------------------------------------------------------------
+@dataclass
+class LayerOps:
+    x: torch.Tensor
+    weight: torch.Tensor
+    positions: torch.Tensor
+    gate: torch.Tensor
+    up: torch.Tensor
+    heads: int = 32
+    head_dim: int = 128
+    theta: float = 1e4
+    eps: float = 1e-5
+
+    @property
+    def rmsnorm_rope_bytes(self) -> int:
+        # x read + y written + weight (tables generated in-kernel)
+        return 2 * self.x.numel() * 2 + self.weight.numel() * 2
+
+    @property
+    def silu_bytes(self) -> int:
+        return 3 * self.gate.numel() * 2
+
+
+def layer_ops(device="cpu", seed: int = 0, tokens: int = 4096, hidden: int = 4096,
+              inter: int = 14336) -> LayerOps:
+    g = _gen(seed)
+    x = _randn(g, tokens, hidden, device=device)
+    w = (1.0 + 0.02 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(device)
+    gate = _randn(g, tokens, inter, device=device)
+    up = _randn(g, tokens, inter, device=device)
+    pos = torch.arange(tokens, device=device).view(1, tokens)
+    return LayerOps(x, w, pos, gate, up)
+
+
+# --------------------------------------------------------------------------------------
+@dataclass
+class RingShare:
+    q: torch.Tensor                        # [1, 8192, 32, 128]
+    q_pos: torch.Tensor                    # [1, 8192]
+    blocks: List[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]]  # by source rank
+    layout: SequenceLayout
+    rank: int
+    kv_sizes: List[int]
+    pairs_per_step: List[int]              # in ring order
+
+    @property
+    def ring_order(self) -> List[int]:
+        n = self.layout.num_ranks
+        return [(self.rank - s) % n for s in range(n)]
+
+    @property
+    def flop(self) -> int:
+        return 4 * self.q.shape[-1] * self.q.shape[2] * sum(self.pairs_per_step)
+
+
+def ring_share(device="cpu", seed: int = 0, seq_len: int = 32768, sp: int = 4, rank: int = 0,
+               hq: int = 32, hkv: int = 8, d: int = 128, dtype=torch.bfloat16) -> RingShare:
+    g = _gen(seed)
+    layout = SequenceLayout(seq_len, sp, kind="zigzag")
+    s_loc = layout.sizes[rank]
+    q = _randn(g, 1, s_loc, hq, d, dtype=dtype, device=device)
+    blocks = []
+    for r in range(sp):
+        n = layout.sizes[r]
+        k = _randn(g, 1, n, hkv, d, dtype=dtype, device=device)
+        v = _randn(g, 1, n, hkv, d, dtype=dtype, device=device)
+        blocks.append((k, v, layout.indices(r).view(1, n).to(device)))
+    q_pos = layout.indices(rank).view(1, s_loc).to(device)
+    order = [(rank - s) % sp for s in range(sp)]
+    pairs = [visible_pairs(q_pos, blocks[r][2]) for r in order]
+    return RingShare(q, q_pos, blocks, layout, rank, list(layout.sizes), pairs)
+
+
+# --------------------------------------------------------------------------------------
+@dataclass
+class KVDecode:
+    q: torch.Tensor                 # [B, 1, Hq, D]
+    q_pos: torch.Tensor             # [B, 1]
+    cache_k: torch.Tensor           # [B, Hkv, cap, D] head-major
+    cache_v: torch.Tensor
+    k_pos: torch.Tensor             # [B, cap] (-1 = unused slot)
+    lengths: torch.Tensor           # [B]
+    part_sizes: List[int]
+    batch: List[int]                # which sequences of the full workload these rows are
+
+    def partitions(self) -> List[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:
+        """Token-major views ``[B, s_p, Hkv, D]`` of each partition (no copies, cache.py:64-74)."""
+        out, start = [], 0
+        for n in self.part_sizes:
+            k = self.cache_k[:, :, start : start + n].transpose(1, 2)
+            v = self.cache_v[:, :, start : start + n].transpose(1, 2)
+            out.append((k, v, self.k_pos[:, start : start + n]))
+            start += n
+        return out
+
+    @property
+    def kv_bytes(self) -> int:
+        hkv, d = self.cache_k.shape[1], self.cache_k.shape[3]
+        return int(self.lengths.sum()) * hkv * d * 2 * self.cache_k.element_size()
+
+    @property
+    def bytes(self) -> int:
+        """Algorithmic HBM bytes of one decode + merge step: valid K/V, the query, every
+        partition's f32 (out, lse) written and read back by the merge, the final output."""
+        B, _, hq, d = self.q.shape
+        n = len(self.part_sizes)
+        q_b = self.q.numel() * self.q.element_size()
+        partial = n * (B * hq * d * 4 + B * hq * 4)
+        return self.kv_bytes + q_b + 2 * partial + q_b
+
+
+def kv_decode(device="cpu", seed: int = 0, batch: Optional[Sequence[int]] = None, B: int = 32,
+              hq: int = 32, hkv: int = 8, d: int = 128, cap: int = 32768,
+              weights=(0.4, 0.3, 0.2, 0.1), min_len: int = 1024,
+              dtype=torch.bfloat16) -> KVDecode:
+    """Cache contents are drawn per sequence (generator ``seed + 1 + b``) for its valid slots
+    only, so any subset of sequences is reproducible on its own; unused slots hold zeros."""
+    g = _gen(seed)
+    lengths_all = torch.randint(min_len, cap + 1, (B,), generator=g)
+    q_all = torch.randn(B, 1, hq, d, generator=g, dtype=torch.float32)
+    rows = list(range(B)) if batch is None else [int(b) for b in batch]
+    nb = len(rows)
+    cache_k = torch.zeros(nb, hkv, cap, d, dtype=dtype, device=device)
+    cache_v = torch.zeros(nb, hkv, cap, d, dtype=dtype, device=device)
+    for i, b in enumerate(rows):
+        L = int(lengths_all[b])
+        gb = _gen(seed + 1 + b)
+        cache_k[i, :, :L] = torch.randn(hkv, L, d, generator=gb).to(dtype).to(device)
+        cache_v[i, :, :L] = torch.randn(hkv, L, d, generator=gb).to(dtype).to(device)
+    lengths = lengths_all[rows]
+    slots = torch.arange(cap).view(1, cap)
+    k_pos = torch.where(slots < lengths.view(-1, 1), slots, torch.full_like(slots, -1)).to(device)
+    q = q_all[rows].to(dtype).to(device)
+    q_pos = (lengths - 1).view(-1, 1).to(device)
+    return KVDecode(q, q_pos, cache_k, cache_v, k_pos, lengths, split_sizes(cap, list(weights)),
+                    rows)
+
+
+# --------------------------------------------------------------------------------------
+@dataclass
+class UlyssesShare:
+    q: torch.Tensor        # [1, S, 8, 128]
+    k: torch.Tensor        # [1, S, 2, 128]
+    v: torch.Tensor
+    pos: torch.Tensor      # [1, S]: 0..L-1 then -1
+    lengths: List[int]
+    kv_map: Optional[Tuple[int, ...]]
+
+    @property
+    def valid(self) -> int:
+        return sum(self.lengths)
+
+    @property
+    def flop(self) -> int:
+        L = self.valid
+        return 4 * self.q.shape[-1] * self.q.shape[2] * L * (L + 1) // 2
+
+
+def ulysses_share(device="cpu", seed: int = 0, seq_len: int = 65536, model_heads=(64, 16),
+                  sp: int = 8, rank: int = 0, d: int = 128, n_seq: int = 4,
+                  dtype=torch.bfloat16) -> UlyssesShare:
+    g = _gen(seed)
+    lengths = [int(x) for x in torch.randint(1, seq_len // n_seq + 1, (n_seq,), generator=g)]
+    shard = partition_heads(model_heads[0], model_heads[1], sp)[rank]
+    q = _randn(g, 1, seq_len, shard.q_count, d, dtype=dtype, device=device)
+    k = _randn(g, 1, seq_len, shard.kv_count, d, dtype=dtype, device=device)
+    v = _randn(g, 1, seq_len, shard.kv_count, d, dtype=dtype, device=device)
+    # positions of packed tokens: where(mask, cumsum(mask) - 1, -1) (engine/engine.py:328-329)
+    mask = torch.arange(seq_len) < sum(lengths)
+    pos = torch.where(mask, torch.cumsum(mask.to(torch.int64), 0) - 1, torch.full((seq_len,), -1))
+    kv_map = tuple(shard.kv_map)
+    return UlyssesShare(q, k, v, pos.view(1, seq_len).to(device), lengths, kv_map)
+
+
+__all__ = [
+    "AttnF32Split",
+    "KVDecode",
+    "LayerOps",
+    "RingShare",
+    "UlyssesShare",
+    "attn_f32_split",
+    "kv_decode",
+    "layer_ops",
+    "ring_share",
+    "ulysses_share",
+    "visible_pairs",
+]

@@ -1,0 +1,181 @@
+/*
+ * collab_edge_attn.h - C ABI of the MI355X (gfx950) attention / LSE / layer-op kernels.
+ *
+ * Every entry point replaces one operator of collab_infer's per-device hot path.  The
+ * reference interface each one stands in for is cited (paths relative to the
+ * collab_infer checkout).  Conventions:
+ *   - all tensors are device pointers described by a cea_tensor (sizes and strides in
+ *     elements, innermost stride must be 1 unless stated otherwise);
+ *   - outputs are allocated by the caller; nothing here allocates device memory;
+ *   - every call is asynchronous on the given stream (a hipStream_t passed as void*,
+ *     NULL = the default stream);
+ *   - the return value is CEA_OK (0) or a negative CEA_E* status; cea_last_error()
+ *     returns the message of the last failure on the calling thread.  Nothing throws.
+ *
+ * Masking is position based: key j is visible to query i iff k_pos[j] >= 0 and
+ * (!causal || k_pos[j] <= q_pos[i]).  Rows without a visible key give out = 0 and
+ * lse = -inf, the neutral element of the merges.
+ */
+#ifndef COLLAB_EDGE_ATTN_H
+#define COLLAB_EDGE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define CEA_F32 0
+#define CEA_BF16 1
+#define CEA_F16 2
+#define CEA_F64 3
+#define CEA_I64 4
+
+/* status codes */
+#define CEA_OK 0
+#define CEA_EINVAL (-1)       /* shape / stride / dtype inconsistency (Python: ValueError)   */
+#define CEA_EUNSUPPORTED (-2) /* valid request the kernels do not cover (NotImplementedError) */
+#define CEA_ELAUNCH (-3)      /* HIP launch or runtime failure (RuntimeError)                 */
+#define CEA_ENOSPACE (-4)     /* workspace smaller than cea_*_workspace_bytes() reported      */
+
+#define CEA_MAX_DIMS 4
+#define CEA_MAX_PARTS 16      /* maximum number of partial results one merge call combines   */
+#define CEA_MAX_MAPPED_HEADS 512 /* maximum query heads when an explicit kv_map is given     */
+
+typedef struct cea_tensor {
+  void* data;                    /* device pointer to element [0, ..., 0]       */
+  int32_t dtype;                 /* CEA_F32 / CEA_BF16 / CEA_F16 / CEA_F64 / CEA_I64 */
+  int32_t ndim;                  /* number of used entries of size / stride    */
+  int64_t size[CEA_MAX_DIMS];
+  int64_t stride[CEA_MAX_DIMS];  /* in elements                                 */
+} cea_tensor;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* cea_last_error(void);
+
+/* Library version as major*10000 + minor*100 + patch. */
+int cea_version(void);
+
+/*
+ * Bytes of device workspace cea_attention_with_lse needs for these shapes (q: [B,Sq,Hq,D],
+ * k: [B,Sk,Hkv,D]).  The workspace holds per-key-tile position summaries and, for short
+ * query blocks, split-KV partial results.
+ */
+size_t cea_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int64_t Hkv,
+                                     int64_t D, int32_t in_dtype);
+
+/*
+ * Masked softmax attention over one KV block returning (out, lse).
+ * Replaces attention_with_lse (collab_infer/parallel/attention.py:201-239) for one KV block:
+ * _flash_lse / _math_lse (attention.py:163-198) with the visibility rule of
+ * visibility_mask (attention.py:96-101) and the GQA mapping of expand_kv / gqa_group
+ * (attention.py:68-93).
+ *   q      [B,Sq,Hq,D]   bf16 / f16 / f32 / f64
+ *   k, v   [B,Sk,Hkv,D]  same dtype as q, any strides with innermost stride 1
+ *   q_pos  [B,Sq] i64,  k_pos [B,Sk] i64
+ *   kv_map host array of Hq entries (query head -> KV head) or NULL for h // (Hq/Hkv)
+ *   out    [B,Sq,Hq,D]   f32 (f64 for f64 inputs), or q's dtype when lse is NULL
+ *                        (the plain attention of attention.py:270-301)
+ *   lse    [B,Hq,Sq]     f32 (f64 for f64 inputs) natural-log log-sum-exp, or NULL
+ *   accumulate  0: write (out, lse);  1: merge this block's result exactly into the
+ *               existing (out, lse) like merge_attention (attention.py:242-250), the
+ *               online merge of ring_attention (sequence_parallel.py:117-121)
+ *   workspace   device buffer of at least cea_attention_workspace_bytes() bytes
+ */
+int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
+                           const cea_tensor* q_pos, const cea_tensor* k_pos, int32_t causal,
+                           double scale, const int32_t* kv_map, int32_t kv_map_len,
+                           cea_tensor* out, cea_tensor* lse, int32_t accumulate,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Pairwise exact merge: lse = logaddexp(lse_a, lse_b); out = out_a*w_a + out_b*w_b.
+ * Replaces merge_attention (collab_infer/parallel/attention.py:242-250).
+ *   out_*  [B,Sq,H,D] f32/f64,  lse_* [B,H,Sq] same dtype.  out may alias out_a (each
+ *   element is read before it is written); lse must not alias an input lse.
+ */
+int cea_merge_attention(const cea_tensor* out_a, const cea_tensor* lse_a, const cea_tensor* out_b,
+                        const cea_tensor* lse_b, cea_tensor* out, cea_tensor* lse, void* stream);
+
+/*
+ * n-way exact merge (n <= CEA_MAX_PARTS): lse = logsumexp_i lse_i; out = sum_i out_i*w_i.
+ * Replaces merge_attention_list (collab_infer/parallel/attention.py:253-264).
+ */
+int cea_merge_attention_list(int32_t n, const cea_tensor* outs, const cea_tensor* lses,
+                             cea_tensor* out, cea_tensor* lse, void* stream);
+
+/*
+ * Attention of one query block against n KV partitions plus the exact merge, in one pass:
+ * the per-device compute of distributed_kv_attention
+ * (collab_infer/parallel/sequence_parallel.py:250-280) for n simulated ranks, with the
+ * all-gather replaced by reading every partition on this device.
+ *   ks, vs, k_pos_s  n tensors, partition p is [B,Sk_p,Hkv,D] with positions [B,Sk_p]
+ *   part_out, part_lse  optional (NULL) arrays of n per-partition results
+ *                       ([B,Sq,Hq,D] / [B,Hq,Sq] f32), i.e. each rank's attention_with_lse
+ *   out    [B,Sq,Hq,D]  q's dtype or f32;  lse [B,Hq,Sq] f32 or NULL
+ */
+size_t cea_partitioned_attention_workspace_bytes(int32_t n, const int64_t* Sk, int64_t B,
+                                                 int64_t Sq, int64_t Hq, int64_t Hkv, int64_t D,
+                                                 int32_t in_dtype);
+int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* ks,
+                              const cea_tensor* vs, const cea_tensor* q_pos,
+                              const cea_tensor* k_pos_s, int32_t causal, double scale,
+                              const int32_t* kv_map, int32_t kv_map_len, cea_tensor* part_out,
+                              cea_tensor* part_lse, cea_tensor* out, cea_tensor* lse,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * RMSNorm over the last dimension with the reference's rounding points:
+ * y = weight * (x * rsqrt(mean(x^2) + eps)).to(x.dtype), computed in f32 (f64 for f64).
+ * Replaces RMSNorm.forward (collab_infer/models/llama.py:52-61).
+ *   x [N,C] (row stride free), weight [C], y [N,C] in promote(weight, x) dtype.
+ */
+int cea_rmsnorm(const cea_tensor* x, const cea_tensor* weight, double eps, cea_tensor* y,
+                void* stream);
+
+/*
+ * Rotary tables at explicit positions: freqs = clamp(pos,0) * inv_freq,
+ * emb = cat(freqs, freqs), cos/sin rounded to the table dtype.
+ * Replaces RotaryEmbedding.forward (collab_infer/models/llama.py:64-77); inv_freq comes
+ * from rope_inv_freq (collab_infer/models/config.py:165-189).
+ *   positions [B,S] i64, inv_freq [D/2] f32 (f64 tables use an f64 inv_freq),
+ *   cos, sin [B,S,D].
+ */
+int cea_rope_tables(const cea_tensor* positions, const cea_tensor* inv_freq, cea_tensor* cos,
+                    cea_tensor* sin, void* stream);
+
+/*
+ * Half-split rotary embedding: out = x*cos + rotate_half(x)*sin with each product and the
+ * sum rounded to x's dtype, as the reference's three tensor ops do.
+ * Replaces apply_rotary / _rotate_half (collab_infer/models/llama.py:80-88).
+ *   x [B,S,H,D], cos/sin [B,S,D] (batch stride may be 0), out [B,S,H,D].
+ */
+int cea_apply_rotary(const cea_tensor* x, const cea_tensor* cos, const cea_tensor* sin,
+                     cea_tensor* out, void* stream);
+
+/*
+ * Fused RMSNorm + rotary: the RMSNorm output of x [S, H*D] viewed as [1,S,H,D] and rotated
+ * at positions [S] with tables generated in-kernel (same rounding points as
+ * cea_rmsnorm followed by cea_rope_tables + cea_apply_rotary).
+ * Replaces the RMSNorm (llama.py:58-61) -> RotaryEmbedding (llama.py:74-77) ->
+ * apply_rotary (llama.py:85-88) sequence.
+ */
+int cea_rmsnorm_rope(const cea_tensor* x, const cea_tensor* weight, double eps,
+                     const cea_tensor* positions, const cea_tensor* inv_freq, int32_t num_heads,
+                     cea_tensor* out, void* stream);
+
+/*
+ * SiLU-gate: out = silu(gate) * up with silu rounded to the tensor dtype before the product.
+ * Replaces act(gate) * up with act = F.silu (collab_infer/models/llama.py:45, 305, 316).
+ *   gate, up [N,I] (row strides free, e.g. column halves of a fused gate/up GEMM output),
+ *   out [N,I].
+ */
+int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COLLAB_EDGE_ATTN_H */

@@ -1,0 +1,155 @@
+"""GPU parity of attention_with_lse / attention / merges against the CPU oracle.
+
+Every case runs the gfx950 kernels through the C ABI (via the package's ctypes binding)
+and compares with oracle.attention_ref on bit-identical inputs; tolerances are stated in
+tests/_cases.py.  The bf16/f16 cases with D in {64, 128} run the MFMA prefill kernel, the
+others the generic kernel.
+"""
+
+import math
+
+import pytest
+import torch
+
+from _cases import Case, assert_attention_close
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # reference known-answer shapes (tests/test_attention.py)
+    Case(2, 7, 7, 4, 4, 8, "aligned", True),
+    Case(2, 7, 7, 4, 4, 8, "aligned", False),
+    Case(1, 9, 9, 6, 2, 4, "aligned", True),
+    Case(1, 9, 9, 6, 2, 4, "aligned", True, kv_map=(0, 0, 0, 1, 1, 1)),
+    Case(1, 4, 4, 2, 2, 4, "left_pad", True),
+    Case(1, 3, 3, 1, 1, 16, "aligned", True),
+    # masks, maps and scales on the MFMA head sizes
+    Case(2, 130, 130, 8, 2, 128, "aligned", True),
+    Case(2, 130, 130, 8, 2, 128, "left_pad", True),
+    Case(1, 200, 200, 4, 4, 128, "right_pad", True),
+    Case(1, 150, 96, 8, 2, 128, "zigzag", True),
+    Case(3, 1, 300, 8, 2, 128, "decode", True),
+    Case(2, 70, 190, 4, 1, 64, "random", True),
+    Case(2, 70, 190, 4, 2, 64, "random", False),
+    Case(1, 64, 64, 4, 3, 128, "aligned", True, kv_map=(0, 2, 1, 1)),
+    Case(1, 100, 100, 2, 2, 64, "aligned", True, scale=-0.05),
+    Case(1, 100, 100, 2, 2, 64, "aligned", True, scale=0.0),
+    Case(1, 33, 65, 2, 1, 128, "all_pad", True),
+    Case(1, 257, 257, 2, 1, 96, "aligned", True),
+]
+
+DTYPES = [torch.float64, torch.float32, torch.bfloat16, torch.float16]
+
+
+def _ids(c):
+    return str(c)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", CASES, ids=_ids)
+def test_attention_with_lse_matches_oracle(cea, dev, case, dtype):
+    q, k, v, qp, kp = case.tensors(dtype)
+    out, lse = cea.attention_with_lse(q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev),
+                                      causal=case.causal, scale=case.scale, kv_map=case.kv_map)
+    # torch's CPU flash operator returns NaN for scale <= 0; the math route evaluates the
+    # defined softmax(scale * q.k) there (and is exact in f64)
+    route = "math" if dtype == torch.float64 or (case.scale is not None and case.scale <= 0) else "flash"
+    ro, rl = ref.attention_with_lse(q, k, v, qp, kp, causal=case.causal, scale=case.scale,
+                                    kv_map=case.kv_map, route=route)
+    torch.cuda.synchronize()
+    assert out.dtype == ref.acc_dtype(dtype) and lse.dtype == ref.acc_dtype(dtype)
+    assert_attention_close(out, lse, ro, rl, dtype, str(case))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["float32", "bfloat16"])
+@pytest.mark.parametrize("case", [CASES[0], CASES[6], CASES[9], CASES[11]], ids=_ids)
+def test_plain_attention_matches_oracle(cea, dev, case, dtype):
+    q, k, v, qp, kp = case.tensors(dtype)
+    out = cea.attention.attention(q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev),
+                                  causal=case.causal, kv_map=case.kv_map)
+    ro = ref.plain_attention(q, k, v, qp, kp, causal=case.causal, kv_map=case.kv_map)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    err = (out.cpu().double() - ro.double()).abs().max().item()
+    if dtype == torch.float32:
+        err /= ro.abs().max().item()
+    assert err <= tol, err
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_split_kv_merged_equals_unsplit(cea, dev, dtype):
+    """Merged disjoint key sets == full attention (tests/test_attention.py:37-49), through
+    merge_attention_list, chained merge_attention and the in-epilogue online merge."""
+    case = Case(2, 96, 160, 8, 2, 128 if dtype in (torch.bfloat16, torch.float16) else 16,
+                "aligned" if False else "random", True, seed=7)
+    q, k, v, qp, kp = case.tensors(dtype)
+    qd, kd, vd, qpd, kpd = (t.to(dev) for t in (q, k, v, qp, kp))
+    full, full_lse = cea.attention_with_lse(qd, kd, vd, qpd, kpd)
+    idx = torch.randperm(case.Sk, generator=torch.Generator().manual_seed(0))
+    parts = [idx[:30], idx[30:101], idx[101:]]
+    res = [cea.attention_with_lse(qd, kd[:, p.to(dev)], vd[:, p.to(dev)], qpd, kpd[:, p.to(dev)])
+           for p in parts]
+    out, lse = cea.merge_attention_list([r[0] for r in res], [r[1] for r in res])
+    o2, l2 = cea.merge_attention(*cea.merge_attention(res[0][0], res[0][1], res[1][0], res[1][1]),
+                                 res[2][0], res[2][1])
+    acc = ref.acc_dtype(dtype)
+    o3 = torch.zeros_like(full)
+    l3 = torch.full_like(full_lse, float("-inf"))
+    for p in parts:
+        cea.attention_with_lse_into(o3, l3, qd, kd[:, p.to(dev)], vd[:, p.to(dev)], qpd, kpd[:, p.to(dev)])
+    ro, rl = ref.attention_with_lse(q, k, v, qp, kp, route="math" if dtype == torch.float64 else "flash")
+    torch.cuda.synchronize()
+    for o, l, name in ((out, lse, "list"), (o2, l2, "pairwise"), (o3, l3, "online")):
+        assert o.dtype == acc
+        assert_attention_close(o, l, full, full_lse, dtype, name)
+        assert_attention_close(o, l, ro, rl, dtype, name + " vs oracle")
+
+
+def test_merge_with_empty_partial_is_identity(cea, dev):
+    """tests/test_attention.py:52-63: padded rows are (0, -inf); merging an empty partial
+    (Sk = 0) changes nothing."""
+    case = Case(1, 4, 4, 2, 2, 4, "left_pad", True, seed=10)
+    q, k, v, qp, kp = case.tensors(torch.float64)
+    qd, kd, vd, qpd, kpd = (t.to(dev) for t in (q, k, v, qp, kp))
+    out, lse = cea.attention_with_lse(qd, kd, vd, qpd, kpd)
+    assert torch.isfinite(out).all()
+    empty_o, empty_l = cea.attention_with_lse(qd, kd[:, :0], vd[:, :0], qpd, kpd[:, :0])
+    merged, mlse = cea.merge_attention(out, lse, empty_o, empty_l)
+    torch.cuda.synchronize()
+    assert torch.equal(merged.cpu(), out.cpu())
+    assert torch.equal(mlse.cpu(), lse.cpu())
+
+
+def test_default_scale(cea, dev):
+    case = Case(1, 3, 3, 1, 1, 16, "aligned", True, seed=13)
+    q, k, v, qp, kp = (t.to(dev) for t in case.tensors(torch.float64))
+    a = cea.attention.attention(q, k, v, qp, kp)
+    b = cea.attention.attention(q, k, v, qp, kp, scale=1 / math.sqrt(16))
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bfloat16", "float32"])
+def test_head_major_cache_views_and_kv_block(cea, dev, dtype):
+    """Token-major views of a head-major [B, H, cap, D] cache (models/cache.py:64-74) are read
+    in place; kv_block gives the same result as one block (attention.py:225-236)."""
+    g = torch.Generator().manual_seed(3)
+    B, Hq, Hkv, cap, D, T = 2, 8, 2, 300, 128, 257
+    ck = torch.randn(B, Hkv, cap, D, generator=g).to(dtype)
+    cv = torch.randn(B, Hkv, cap, D, generator=g).to(dtype)
+    q = torch.randn(B, 5, Hq, D, generator=g).to(dtype)
+    kpos = torch.arange(T).repeat(B, 1)
+    qpos = torch.arange(T - 5, T).repeat(B, 1)
+    kview = ck[:, :, :T].transpose(1, 2)
+    vview = cv[:, :, :T].transpose(1, 2)
+    ckd, cvd = ck.to(dev), cv.to(dev)
+    kd, vd = ckd[:, :, :T].transpose(1, 2), cvd[:, :, :T].transpose(1, 2)
+    assert not kd.is_contiguous()
+    out, lse = cea.attention_with_lse(q.to(dev), kd, vd, qpos.to(dev), kpos.to(dev))
+    ob, lb = cea.attention_with_lse(q.to(dev), kd, vd, qpos.to(dev), kpos.to(dev), kv_block=64)
+    ro, rl = ref.attention_with_lse(q, kview, vview, qpos, kpos)
+    torch.cuda.synchronize()
+    assert_attention_close(out, lse, ro, rl, dtype, "cache view")
+    assert_attention_close(ob, lb, ro, rl, dtype, "cache view kv_block")
