@@ -15,14 +15,20 @@
 //   * O^T += V^T.P^T with the same instruction (A = V^T from LDS, B = P from registers):
 //     the score accumulator is already in B-operand order once V^T is stored with the
 //     key-slot permutation below, so P never leaves the registers;
-//   * K and V^T tiles are double-buffered in LDS (global -> VGPR -> LDS; V is transposed on
-//     the way), XOR-swizzled so both the 16-byte fragment reads and the tile writes are
-//     free of bank conflicts;
-//   * softmax runs in the exp2 domain with log2(e)*scale folded into one FMA per score;
+//   * K tiles go global -> LDS directly (buffer_load ... lds, no VGPR staging); V tiles go
+//     through VGPRs and are transposed into V^T on the LDS write; both are double-buffered
+//     and XOR-swizzled so 16-byte fragment reads and tile writes are bank-conflict free;
+//   * buffer resources clamp reads past the last key to zero, so partial tiles need no
+//     branches; the tile base lives in the resource (scalar), lane offsets are constants;
+//   * softmax runs in the exp2 domain with log2(e)*scale folded into one FMA per score, and
+//     the running maximum is only moved (and O rescaled) when a row's maximum grows by more
+//     than 2^8 - the result is exact either way because l and O share the reference max;
 //   * a 64-key tile is skipped, computed unmasked, or computed with an element mask,
 //     decided per wave from the tile's position summary (min/max valid position, count)
 //     and the wave's query-position range, so causal, zigzag and padding masks cost nothing
 //     on tiles that are entirely visible or entirely hidden.
+#include <type_traits>
+
 #include "cea_kernels.hpp"
 
 namespace cea {
@@ -31,6 +37,9 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16> {
@@ -46,9 +55,11 @@ template <> struct Mfma<f16> {
   }
 };
 
-constexpr int BM = 128;       // query rows per workgroup
-constexpr int BN = kTileKeys; // keys per tile
+constexpr int BM = 128;        // query rows per workgroup
+constexpr int BN = kTileKeys;  // keys per tile
 constexpr int NTHREADS = 256;
+constexpr float kRescaleLog2 = 8.0f;        // lazy-rescale threshold, log2 units
+constexpr int kRsrcFlags = 0x00020000;      // raw buffer resource word 3 (gfx9 family)
 
 template <int D> struct Layout {
   static constexpr int KROW = D * 2;                 // bytes per K row
@@ -58,7 +69,8 @@ template <int D> struct Layout {
   static constexpr int POS_BYTES = BN * 8;
   static constexpr int BUF_BYTES = K_BYTES + VT_BYTES + POS_BYTES;
   static constexpr int LDS_BYTES = 2 * BUF_BYTES;
-  static constexpr int K_CHUNKS = BN * NCG / NTHREADS;  // 16-byte K chunks per thread
+  static constexpr int K_LOADS = K_BYTES / (NTHREADS * 16);  // direct loads per wave
+  static constexpr int KEYS_PER_LOAD = 1024 / KROW;          // keys per wave load
 };
 
 // K row swizzle: 16-byte group g of key row 'key' lives at group (g ^ swz(key)).
@@ -75,8 +87,32 @@ __device__ __forceinline__ int vt_slot(int key) {
   return (key & ~15) | (((key >> 2) & 1) << 3) | (((key >> 3) & 1) << 2) | (key & 3);
 }
 
-__device__ __forceinline__ int64_t lds_i64(const char* base, int idx) {
-  return *(const int64_t*)(base + idx * 8);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRsrcFlags);
+}
+
+// 16 bytes per lane from a buffer straight into LDS at lds_base + lane*16.  Kept out of
+// lambdas: used inside one, the builtin makes the host pass drop the kernel's launch stub.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rs, char* lds_base,
+                                                  uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)lds_base, 16, voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
+}
+
+// max of x over the two 32-lane halves of the wave (v_permlane32_swap)
+__device__ __forceinline__ float max_halves(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
 template <typename T, int D>
@@ -109,8 +145,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   const int64_t qpos = row_ok ? p.q_pos[b * p.qps_b + (int64_t)row * p.qps_s] : 0;
 
   // ---- query position ranges of the wave and of the workgroup
-  int64_t qmin_w = wave_min_i64(row_ok ? qpos : INT64_MAX);
-  int64_t qmax_w = wave_max_i64(row_ok ? qpos : INT64_MIN);
+  const int64_t qmin_w = wave_min_i64(row_ok ? qpos : INT64_MAX);
+  const int64_t qmax_w = wave_max_i64(row_ok ? qpos : INT64_MIN);
   const bool wave_active = __builtin_amdgcn_readfirstlane(qb * BM + wave * 32 < p.Sq ? 1 : 0);
   if (lane == 0) {
     red_q[0][wave] = qmin_w;
@@ -123,6 +159,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   // scale is absorbed by negating Q (exact in bf16/f16).
   const float scale = (float)p.scale;
   const float c = fabsf(scale) * 1.4426950408889634f;
+  const float grow_thr = kRescaleLog2 / c;  // raw-score growth that triggers a rescale
   const uint32_t qflip = scale < 0.f ? 0x80008000u : 0u;
 
   frag qf[D / 16];
@@ -137,10 +174,46 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     }
   }
 
-  const T* kbase = (const T*)p.k + b * p.ks_b + kvh * p.ks_h;
-  const T* vbase = (const T*)p.v + b * p.vs_b + kvh * p.vs_h;
+  const char* kbase = (const char*)((const T*)p.k + b * p.ks_b + kvh * p.ks_h);
+  const char* vbase = (const char*)((const T*)p.v + b * p.vs_b + kvh * p.vs_h);
   const int64_t* kpos_b = p.k_pos + b * p.kps_b;
   const TileInfo* tinfo = p.tiles + (int64_t)b * p.ntiles;
+  const uint32_t krow_bytes = (uint32_t)(p.ks_s * 2), vrow_bytes = (uint32_t)(p.vs_s * 2);
+
+  // ---- per-lane constant offsets
+  // direct K loads: wave load i covers keys (wave*K_LOADS+i)*KEYS_PER_LOAD ...; lane l writes
+  // LDS bytes l*16 of that 1 KB and so must fetch logical group (l % NCG) ^ swz(key)
+  uint32_t k_voff[L::K_LOADS];
+#pragma unroll
+  for (int i = 0; i < L::K_LOADS; ++i) {
+    const int key = (wave * L::K_LOADS + i) * L::KEYS_PER_LOAD + lane / L::NCG;
+    const int cg = (lane % L::NCG) ^ k_swz<D>(key);
+    k_voff[i] = key * krow_bytes + cg * 16;
+  }
+  // V: lane owns 4 consecutive keys x 8 features; transposed LDS writes
+  const int v_kq = (lane >> 1) & 15;
+  const int v_c = (lane & 1) + 2 * (lane >> 5) + 4 * wave;  // 8-feature chunk of V
+  const bool v_on = v_c < D / 8;
+  uint32_t v_voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v_voff[j] = (v_kq * 4 + j) * vrow_bytes + v_c * 16;
+  uint32_t v_waddr[8];
+  {
+    const int slot = vt_slot(v_kq * 4);
+    const int cgv = slot >> 3, within = (slot & 7) * 2;
+#pragma unroll
+    for (int dd = 0; dd < 8; ++dd) {
+      const int d = v_c * 8 + (dd ^ (v_c & 1));  // alternate row order between lane pairs
+      v_waddr[dd] = L::K_BYTES + d * 128 + ((cgv ^ vt_swz(d)) << 4) + within;
+    }
+  }
+  // fragment reads
+  uint32_t k_raddr[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) k_raddr[ks] = r * L::KROW + (((2 * ks + g) ^ k_swz<D>(r)) << 4);
+  uint32_t v_raddr[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) v_raddr[s] = L::K_BYTES + r * 128 + (((2 * s + g) ^ vt_swz(r)) << 4);
 
   // ---- list of tiles the workgroup visits: 64 summaries per ballot
   int chunk_base = -64;
@@ -162,64 +235,38 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     return __builtin_amdgcn_readfirstlane(t);
   };
 
-  // ---- tile staging: K as 16-byte chunks, V as 4-key x 8-feature blocks (transposed)
-  uint4 kreg[L::K_CHUNKS];
-  uint4 vreg[4];
+  u32x4 vreg[4];
   int64_t preg = -1;
-  const int v_kq = (lane >> 1) & 15;
-  const int v_c = (lane & 1) + 2 * (lane >> 5) + 4 * wave;  // 8-feature chunk of V
-  const bool v_on = v_c < D / 8;
-
-  auto load_tile = [&](int t) {
+  // issue the global reads of tile t: K straight into LDS buffer 'bo', V and positions to VGPRs
+  auto load_tile = [&](int t, int bo) {
     const int key0 = t * BN;
+    const int left = p.Sk - key0;  // > 0 for every visited tile
+    const uint32_t kbytes = (uint32_t)(left - 1) * krow_bytes + L::KROW;
+    const uint32_t vbytes = (uint32_t)(left - 1) * vrow_bytes + L::KROW;
+    const auto krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, kbytes);
+    const auto vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, vbytes);
 #pragma unroll
-    for (int i = 0; i < L::K_CHUNKS; ++i) {
-      const int q = tid + i * NTHREADS;
-      const int key = q / L::NCG, cg = q % L::NCG;
-      kreg[i] = make_uint4(0, 0, 0, 0);
-      if (key0 + key < p.Sk)
-        kreg[i] = *(const uint4*)(kbase + (int64_t)(key0 + key) * p.ks_s + cg * 8);
-    }
+    for (int i = 0; i < L::K_LOADS; ++i)
+      buffer_load_lds16(krs, smem + bo + (wave * L::K_LOADS + i) * 1024, k_voff[i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int key = key0 + v_kq * 4 + j;
-      vreg[j] = make_uint4(0, 0, 0, 0);
-      if (v_on && key < p.Sk) vreg[j] = *(const uint4*)(vbase + (int64_t)key * p.vs_s + v_c * 8);
-    }
-    if (tid < BN) {
-      const int key = key0 + tid;
-      preg = key < p.Sk ? kpos_b[(int64_t)key * p.kps_s] : -1;
-    }
+    for (int j = 0; j < 4; ++j)
+      vreg[j] = v_on ? __builtin_amdgcn_raw_buffer_load_b128(vrs, v_voff[j], 0, 0) : u32x4{0, 0, 0, 0};
+    if (tid < BN) preg = tid < left ? kpos_b[(int64_t)(key0 + tid) * p.kps_s] : -1;
   };
-
-  auto store_tile = [&](int buf) {
-    char* kl = smem + buf * L::BUF_BYTES;
-    char* vl = kl + L::K_BYTES;
-    char* pl = vl + L::VT_BYTES;
-#pragma unroll
-    for (int i = 0; i < L::K_CHUNKS; ++i) {
-      const int q = tid + i * NTHREADS;
-      const int key = q / L::NCG, cg = q % L::NCG;
-      *(uint4*)(kl + key * L::KROW + ((cg ^ k_swz<D>(key)) << 4)) = kreg[i];
-    }
+  // write the register-staged part of a tile (V^T, positions) into LDS buffer 'bo'
+  auto store_tile = [&](int bo) {
     if (v_on) {
-      const int slot = vt_slot(v_kq * 4);
-      const int cgv = slot >> 3, within = (slot & 7) * 2;
-      const uint32_t* w0 = (const uint32_t*)&vreg[0];
-      const uint32_t* w1 = (const uint32_t*)&vreg[1];
-      const uint32_t* w2 = (const uint32_t*)&vreg[2];
-      const uint32_t* w3 = (const uint32_t*)&vreg[3];
 #pragma unroll
       for (int dd = 0; dd < 8; ++dd) {
-        const int e = dd ^ (v_c & 1);     // row order alternates between lane pairs
-        const int d = v_c * 8 + e;
-        const int sh = (e & 1) * 16;
-        const uint32_t lo = ((w0[e >> 1] >> sh) & 0xffffu) | (((w1[e >> 1] >> sh) & 0xffffu) << 16);
-        const uint32_t hi = ((w2[e >> 1] >> sh) & 0xffffu) | (((w3[e >> 1] >> sh) & 0xffffu) << 16);
-        *(uint2*)(vl + d * 128 + ((cgv ^ vt_swz(d)) << 4) + within) = make_uint2(lo, hi);
+        const int e = dd ^ (v_c & 1);
+        const int wi = e >> 1;
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t lo = __builtin_amdgcn_perm(vreg[1][wi], vreg[0][wi], sel);
+        const uint32_t hi = __builtin_amdgcn_perm(vreg[3][wi], vreg[2][wi], sel);
+        *(u32x2*)(smem + bo + v_waddr[dd]) = u32x2{lo, hi};
       }
     }
-    if (tid < BN) *(int64_t*)(pl + tid * 8) = preg;
+    if (tid < BN) *(int64_t*)(smem + bo + L::K_BYTES + L::VT_BYTES + tid * 8) = preg;
   };
 
   f32x16 oacc[D / 32];
@@ -227,111 +274,123 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   for (int i = 0; i < D / 32; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[i][e] = 0.f;
-  float m_run = -__builtin_inff();  // running max of raw scores (q.k)
+  float m_run = -__builtin_inff();  // reference max of raw scores (q.k)
+  float m_use = 0.f;                // m_run * c, or 0 while the row has seen nothing
   float l_run = 0.f;                // this lane's partial row sum
 
-  int t_cur = next_tile();
-  if (t_cur >= 0) {
-    load_tile(t_cur);
-    store_tile(0);
-  }
-  __syncthreads();
-  int buf = 0;
-  while (t_cur >= 0) {
-    const int t_next = next_tile();
-    if (t_next >= 0) load_tile(t_next);
-
-    // per-wave mode of this tile: 0 skip, 1 full, 2 element-masked
-    const TileInfo ti = tinfo[t_cur];
-    int mode;
+  auto compute = [&](auto bufc, int t) {
+    constexpr int BO = decltype(bufc)::value * L::BUF_BYTES;
+    const TileInfo ti = tinfo[t];
+    int mode;  // 0 skip, 1 full, 2 element-masked
     if (!wave_active || ti.n_valid == 0 || (p.causal && qmax_w < ti.min_valid)) mode = 0;
     else if (ti.n_valid == BN && (!p.causal || ti.max_valid <= qmin_w)) mode = 1;
     else mode = 2;
     mode = __builtin_amdgcn_readfirstlane(mode);
+    if (mode == 0) return;
 
-    if (mode != 0) {
-      const char* kl = smem + buf * L::BUF_BYTES;
-      const char* vl = kl + L::K_BYTES;
-      const char* pl = vl + L::VT_BYTES;
-      f32x16 sacc[2];
+    f32x16 sacc[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb) {
+      frag kf[D / 16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.f;
-        const int key = kb * 32 + r;
-        const char* krow = kl + key * L::KROW;
-        const int sw = k_swz<D>(key);
+      for (int ks = 0; ks < D / 16; ++ks)
+        kf[ks] = *(const frag*)(smem + BO + kb * 32 * L::KROW + k_raddr[ks]);
+      f32x16 acc = {};
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) {
-          const frag kf = *(const frag*)(krow + (((2 * ks + g) ^ sw) << 4));
-          sacc[kb] = Mfma<T>::run(kf, qf[ks], sacc[kb]);
-        }
-      }
-      if (mode == 2) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) {
-            const int key = kb * 32 + i4 * 8 + g * 4;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int64_t kp = lds_i64(pl, key + j);
-              const bool vis = row_ok && kp >= 0 && (!p.causal || kp <= qpos);
-              if (!vis) sacc[kb][i4 * 4 + j] = -__builtin_inff();
-            }
-          }
-      }
-      // online softmax (exp2 domain)
-      float mx = -__builtin_inff();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -__builtin_inff() ? 0.f : m_new * c;
-      const float alpha = __builtin_amdgcn_exp2f(m_run * c - m_use);
-      m_run = m_new;
-      float psum = 0.f;
-      frag pf[4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][e], c, -m_use));
-          psum += pv;
-          pf[kb * 2 + (e >> 3)][e & 7] = (T)pv;
-        }
-      l_run = l_run * alpha + psum;
-      if (__ballot(alpha != 1.f) != 0) {
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
-      }
-      // O^T += V^T . P^T
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        const int d = dt * 32 + r;
-        const char* vrow = vl + d * 128;
-        const int sw = vt_swz(d);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const frag vf = *(const frag*)(vrow + (((2 * s + g) ^ sw) << 4));
-          oacc[dt] = Mfma<T>::run(vf, pf[s], oacc[dt]);
-        }
-      }
+      for (int ks = 0; ks < D / 16; ++ks) acc = Mfma<T>::run(kf[ks], qf[ks], acc);
+      sacc[kb] = acc;
     }
-    if (t_next < 0) break;
-    store_tile(buf ^ 1);
+    if (mode == 2) {
+      const char* pl = smem + BO + L::K_BYTES + L::VT_BYTES + g * 32;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int64_t kp = *(const int64_t*)(pl + (kb * 32 + i4 * 8 + j) * 8);
+            const bool vis = row_ok && kp >= 0 && (!p.causal || kp <= qpos);
+            if (!vis) sacc[kb][i4 * 4 + j] = -__builtin_inff();
+          }
+        }
+    }
+    // online softmax (exp2 domain) with a lazily moved reference maximum
+    float mx = max3f(sacc[0][0], sacc[0][1], sacc[0][2]);
+#pragma unroll
+    for (int e = 3; e < 15; e += 2) mx = max3f(mx, sacc[0][e], sacc[0][e + 1]);
+    mx = max3f(mx, sacc[0][15], sacc[1][0]);
+#pragma unroll
+    for (int e = 1; e < 15; e += 2) mx = max3f(mx, sacc[1][e], sacc[1][e + 1]);
+    mx = __builtin_fmaxf(mx, sacc[1][15]);
+    mx = max_halves(mx);
+    const bool grow = mx > m_run + grow_thr;
+    if (__ballot(grow) != 0) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = grow ? __builtin_amdgcn_exp2f((m_run - m_new) * c) : 1.f;
+      m_run = m_new;
+      m_use = m_run == -__builtin_inff() ? 0.f : m_run * c;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
+    }
+    float psum = 0.f;
+    frag pf[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][e], c, -m_use));
+        psum += pv;
+        pf[kb * 2 + (e >> 3)][e & 7] = (T)pv;
+      }
+    l_run += psum;
+    // O^T += V^T . P^T
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      frag vf[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) vf[s] = *(const frag*)(smem + BO + dt * 32 * 128 + v_raddr[s]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) oacc[dt] = Mfma<T>::run(vf[s], pf[s], oacc[dt]);
+    }
+  };
+
+  auto sync_tile = [&]() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    buf ^= 1;
+  };
+
+  int t_cur = next_tile();
+  if (t_cur >= 0) {
+    load_tile(t_cur, 0);
+    store_tile(0);
+  }
+  sync_tile();
+  // two-stage software pipeline, unrolled so each stage reads one LDS buffer with
+  // immediate offsets: buffer 0 holds t_cur on entry of the first stage
+  while (t_cur >= 0) {
+    int t_next = next_tile();
+    if (t_next >= 0) load_tile(t_next, L::BUF_BYTES);
+    compute(std::integral_constant<int, 0>(), t_cur);
+    if (t_next < 0) break;
+    store_tile(L::BUF_BYTES);
+    sync_tile();
+    t_cur = t_next;
+
+    t_next = next_tile();
+    if (t_next >= 0) load_tile(t_next, 0);
+    compute(std::integral_constant<int, 1>(), t_cur);
+    if (t_next < 0) break;
+    store_tile(0);
+    sync_tile();
     t_cur = t_next;
   }
 
   // ---- epilogue: normalise, emit (out, lse) or merge them into the running pair
   if (!row_ok) return;
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = sum_halves(l_run);
   const bool empty = !(l_tot > 0.f);
   const float inv = empty ? 0.f : 1.f / l_tot;
   const float lse_new = empty ? -__builtin_inff() : m_run * fabsf(scale) + logf(l_tot);
@@ -349,8 +408,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
       for (int i4 = 0; i4 < 4; ++i4) {
         float4* dst = (float4*)(orow + dt * 32 + i4 * 8 + g * 4);
         float4 prev = *dst;
-        float o0 = oacc[dt][i4 * 4 + 0] * inv, o1 = oacc[dt][i4 * 4 + 1] * inv;
-        float o2 = oacc[dt][i4 * 4 + 2] * inv, o3 = oacc[dt][i4 * 4 + 3] * inv;
+        const float o0 = oacc[dt][i4 * 4 + 0] * inv, o1 = oacc[dt][i4 * 4 + 1] * inv;
+        const float o2 = oacc[dt][i4 * 4 + 2] * inv, o3 = oacc[dt][i4 * 4 + 3] * inv;
         prev.x = add_rn(mul_rn(prev.x, w_old), mul_rn(o0, w_new));
         prev.y = add_rn(mul_rn(prev.y, w_old), mul_rn(o1, w_new));
         prev.z = add_rn(mul_rn(prev.z, w_old), mul_rn(o2, w_new));
@@ -428,7 +487,13 @@ bool prefill_mfma_supported(const AttnParams& p) {
   if (!al16(p.q) || !al16(p.k) || !al16(p.v) || !al16(p.out)) return false;
   const int64_t so[] = {p.os_b, p.os_s, p.os_h};
   for (int64_t s : so)
-    if (s % (p.out_dtype == CEA_F32 ? 4 : 4)) return false;
+    if (s % 4) return false;
+  // buffer resources address one (batch, kv head) block with 32-bit offsets: rows must not
+  // overlap and the block must stay below 2 GiB
+  if (p.ks_s < p.D || p.vs_s < p.D) return false;
+  const int64_t kspan = ((int64_t)p.Sk - 1) * p.ks_s * 2 + p.D * 2;
+  const int64_t vspan = ((int64_t)p.Sk - 1) * p.vs_s * 2 + p.D * 2;
+  if (kspan >= ((int64_t)1 << 31) || vspan >= ((int64_t)1 << 31)) return false;
   return true;
 }
 

@@ -1,0 +1,132 @@
+"""The C ABI library: it loads, exports every function include/collab_edge_attn.h declares,
+and rejects inconsistent arguments with the documented status codes before any device work
+(argument validation only: no kernel runs here)."""
+
+import ctypes
+import subprocess
+
+import pytest
+import torch
+
+from conftest import PKG
+
+
+def test_header_lists_the_entry_points(cea):
+    names = cea._native.header_symbols()
+    for expected in ("cea_attention_with_lse", "cea_merge_attention", "cea_merge_attention_list",
+                     "cea_partitioned_attention", "cea_rmsnorm", "cea_rope_tables",
+                     "cea_apply_rotary", "cea_rmsnorm_rope", "cea_silu_mul", "cea_last_error"):
+        assert expected in names
+
+
+def test_library_loads_and_exports_every_header_symbol(cea):
+    lib_path = cea._native.LIB_PATH
+    assert lib_path.exists(), "build the library first (__graft_entry__.build())"
+    raw = ctypes.CDLL(str(lib_path))  # fails on unresolved symbols (RTLD_NOW semantics below)
+    for name in cea._native.header_symbols():
+        assert hasattr(raw, name), f"{name} declared in the header but not exported"
+    # every undefined symbol must come from a system / ROCm library, never from our own code
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(lib_path)], capture_output=True, text=True)
+    own = [l for l in out.stdout.splitlines() if "cea" in l]
+    assert not own, f"unresolved library-internal symbols: {own}"
+
+
+def test_version(cea):
+    assert cea._native.load_library().cea_version() >= 100
+
+
+def _t(shape, dtype_code, data=0x1000):
+    a = cea_tensor = None
+    import importlib
+
+    nat = importlib.import_module(PKG + "._native")
+    a = nat.CeaTensor()
+    a.data = data
+    a.dtype = dtype_code
+    a.ndim = len(shape)
+    stride = 1
+    for i in reversed(range(len(shape))):
+        a.size[i] = shape[i]
+        a.stride[i] = stride
+        stride *= shape[i]
+    return a
+
+
+def test_attention_rejects_bad_shapes_without_launching(cea):
+    nat = cea._native
+    lib = nat.load_library()
+    bf16, i64, f32 = 1, 4, 0
+    q = _t((1, 4, 4, 8), bf16)
+    k = _t((1, 5, 3, 8), bf16)   # 4 query heads cannot share 3 KV heads evenly
+    v = _t((1, 5, 3, 8), bf16)
+    qp, kp = _t((1, 4), i64), _t((1, 5), i64)
+    out, lse = _t((1, 4, 4, 8), f32), _t((1, 4, 4), f32)
+    rc = lib.cea_attention_with_lse(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), ctypes.byref(qp),
+                                    ctypes.byref(kp), 1, 0.125, None, 0, ctypes.byref(out),
+                                    ctypes.byref(lse), 0, None, 0, None)
+    assert rc == nat.EINVAL
+    assert "cannot share" in nat.last_error()
+    with pytest.raises(ValueError, match="cannot share"):
+        nat.check(rc, "attention_with_lse")
+    # explicit map of the wrong length
+    arr = (ctypes.c_int32 * 3)(0, 1, 2)
+    rc = lib.cea_attention_with_lse(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), ctypes.byref(qp),
+                                    ctypes.byref(kp), 1, 0.125, arr, 3, ctypes.byref(out),
+                                    ctypes.byref(lse), 0, None, 0, None)
+    assert rc == nat.EINVAL and "one entry per query head" in nat.last_error()
+    # lse of the wrong shape
+    bad_lse = _t((1, 4, 5), f32)
+    k2, v2 = _t((1, 5, 2, 8), bf16), _t((1, 5, 2, 8), bf16)
+    rc = lib.cea_attention_with_lse(ctypes.byref(q), ctypes.byref(k2), ctypes.byref(v2), ctypes.byref(qp),
+                                    ctypes.byref(kp), 1, 0.125, None, 0, ctypes.byref(out),
+                                    ctypes.byref(bad_lse), 0, None, 0, None)
+    assert rc == nat.EINVAL and "lse must be" in nat.last_error()
+
+
+def test_merge_rejects_too_many_parts_and_bad_dtypes(cea):
+    nat = cea._native
+    lib = nat.load_library()
+    outs = (nat.CeaTensor * 17)(*[_t((1, 2, 2, 4), 0) for _ in range(17)])
+    lses = (nat.CeaTensor * 17)(*[_t((1, 2, 2), 0) for _ in range(17)])
+    o, l = _t((1, 2, 2, 4), 0), _t((1, 2, 2), 0)
+    rc = lib.cea_merge_attention_list(17, outs, lses, ctypes.byref(o), ctypes.byref(l), None)
+    assert rc == nat.EUNSUPPORTED
+    b = (nat.CeaTensor * 2)(_t((1, 2, 2, 4), 1), _t((1, 2, 2, 4), 1))
+    rc = lib.cea_merge_attention_list(2, b, lses, ctypes.byref(o), ctypes.byref(l), None)
+    assert rc == nat.EUNSUPPORTED and "float32 or float64" in nat.last_error()
+
+
+def test_layer_ops_reject_bad_shapes(cea):
+    nat = cea._native
+    lib = nat.load_library()
+    x, w, y = _t((4, 8), 1), _t((7,), 1), _t((4, 8), 1)
+    rc = lib.cea_rmsnorm(ctypes.byref(x), ctypes.byref(w), 1e-5, ctypes.byref(y), None)
+    assert rc == nat.EINVAL and "weight" in nat.last_error()
+    x4 = _t((1, 2, 2, 7), 1)
+    cs = _t((1, 2, 7), 1)
+    rc = lib.cea_apply_rotary(ctypes.byref(x4), ctypes.byref(cs), ctypes.byref(cs), ctypes.byref(x4), None)
+    assert rc == nat.EINVAL and "even" in nat.last_error()
+    g, u = _t((4, 8), 1), _t((4, 9), 1)
+    rc = lib.cea_silu_mul(ctypes.byref(g), ctypes.byref(u), ctypes.byref(g), None)
+    assert rc == nat.EINVAL
+
+
+def test_python_api_refuses_host_tensors(cea):
+    q = torch.zeros(1, 2, 2, 8, dtype=torch.bfloat16)
+    p = torch.arange(2).view(1, 2)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        cea.attention_with_lse(q, q, q, p, p)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        cea.rmsnorm(q.view(4, 8), torch.ones(8, dtype=torch.bfloat16), 1e-5)
+
+
+def test_python_api_validates_heads_before_device_work(cea):
+    q = torch.zeros(1, 2, 4, 8)
+    k = torch.zeros(1, 2, 3, 8)
+    with pytest.raises(ValueError, match="cannot share"):
+        cea.expand_kv(k, 4)
+    assert cea.gqa_group(8, 2) == 4
+    assert cea.gqa_group(8, 2, [0, 0, 0, 0, 1, 1, 1, 1]) == 4
+    assert cea.gqa_group(8, 2, [0, 1, 0, 1, 0, 1, 0, 1]) is None
+    with pytest.raises(ValueError, match="one entry per query head"):
+        cea.expand_kv(k, 4, kv_map=[0, 1])
