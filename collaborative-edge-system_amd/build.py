@@ -44,7 +44,8 @@ COMMON_FLAGS = [
 # NaN; without NaN semantics the compiler drops the quieting v_max_f32 x,x,x it otherwise
 # puts on every matrix-core result before a max.
 FILE_FLAGS = {
-    "attn_prefill.hip": ["-fno-honor-nans"],
+    # M0 is set by the kernel's own LDS-DMA assembly; the clobber note is expected
+    "attn_prefill.hip": ["-fno-honor-nans", "-Wno-inline-asm"],
 }
 
 

@@ -7,28 +7,27 @@
 // optionally the exact online merge of merge_attention (attention.py:242-250) into a running
 // (out, lse) pair, as ring_attention does per step (sequence_parallel.py:117-121).
 //
-// Tiling (one workgroup = 4 waves = 128 query rows of one query head):
+// Structure (one workgroup = 8 waves = 256 query rows of one query head, one per CU):
 //   * every wave owns 32 query rows; its Q fragment stays in VGPRs for the whole kernel;
 //   * S^T = K.Q^T per 64-key tile with v_mfma_f32_32x32x16 (A = K from LDS, B = Q):
 //     lane (r, g) of the accumulator holds query row r and 16 of the 32 keys of a sub-tile,
 //     so the row statistics of the online softmax are per-lane scalars;
-//   * O^T += V^T.P^T with the same instruction (A = V^T from LDS, B = P from registers):
-//     the score accumulator is already in B-operand order once V^T is stored with the
-//     key-slot permutation below, so P never leaves the registers;
-//   * K tiles go global -> LDS directly (buffer_load ... lds, no VGPR staging); V tiles go
-//     through VGPRs and are transposed into V^T on the LDS write; both are double-buffered
-//     and XOR-swizzled so 16-byte fragment reads and tile writes are bank-conflict free;
-//   * buffer resources clamp reads past the last key to zero, so partial tiles need no
-//     branches; the tile base lives in the resource (scalar), lane offsets are constants;
+//   * O^T += V^T.P^T with the same instruction (A = V^T, B = P straight from the score
+//     registers): V stays row-major in LDS and ds_read_b64_tr_b16 transposes it on the way
+//     to the registers (each 16-lane group turns 16 x 4 elements into 4 keys of 16 columns);
+//   * K, V and the key positions of a tile go global -> LDS directly (buffer_load ... lds),
+//     through a 4-stage ring of LDS buffers with 3 tiles in flight, so HBM/L2 latency is
+//     hidden behind two tiles of matrix work; buffer resources return zero past the last
+//     key, so partial tiles need no branches;
+//   * K rows are XOR-swizzled in 16-byte groups and V rows in 64-byte blocks, which keeps
+//     both the fragment reads and the transposing reads free of LDS bank conflicts;
 //   * softmax runs in the exp2 domain with log2(e)*scale folded into one FMA per score, and
-//     the running maximum is only moved (and O rescaled) when a row's maximum grows by more
-//     than 2^8 - the result is exact either way because l and O share the reference max;
-//   * a 64-key tile is skipped, computed unmasked, or computed with an element mask,
-//     decided per wave from the tile's position summary (min/max valid position, count)
-//     and the wave's query-position range, so causal, zigzag and padding masks cost nothing
-//     on tiles that are entirely visible or entirely hidden.
-#include <type_traits>
-
+//     the running maximum only moves (and O is only rescaled) when a row's maximum grows
+//     by more than 2^8; l and O share that reference maximum, so the result is exact;
+//   * the tiles a workgroup visits are listed up front from per-tile position summaries;
+//     each wave then computes a tile unmasked, element-masked or not at all from its own
+//     query-position range, so causal, zigzag and padding masks cost nothing on tiles that
+//     are entirely visible or entirely hidden.
 #include "cea_kernels.hpp"
 
 namespace cea {
@@ -37,9 +36,9 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16> {
@@ -55,55 +54,92 @@ template <> struct Mfma<f16> {
   }
 };
 
-constexpr int BM = 128;        // query rows per workgroup
-constexpr int BN = kTileKeys;  // keys per tile
-constexpr int NTHREADS = 256;
-constexpr float kRescaleLog2 = 8.0f;        // lazy-rescale threshold, log2 units
-constexpr int kRsrcFlags = 0x00020000;      // raw buffer resource word 3 (gfx9 family)
+constexpr int NWAVES = 8;
+constexpr int NTHREADS = NWAVES * 64;
+constexpr int BM = NWAVES * 32;   // query rows per workgroup
+constexpr int BN = kTileKeys;     // keys per tile
+constexpr int NSTAGE = 4;         // LDS ring depth (NSTAGE - 1 tiles in flight)
+constexpr int LIST_CAP = 2048;    // tiles listed per pass over the key block
+constexpr float kRescaleLog2 = 8.0f;    // lazy-rescale threshold, log2 units
+constexpr int kRsrcFlags = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 
 template <int D> struct Layout {
-  static constexpr int KROW = D * 2;                 // bytes per K row
-  static constexpr int NCG = D / 8;                  // 16-byte groups per K row
+  static constexpr int KROW = D * 2;                 // bytes per K / V row
+  static constexpr int NCG = D / 8;                  // 16-byte groups per row
   static constexpr int K_BYTES = BN * KROW;
-  static constexpr int VT_BYTES = D * BN * 2;        // V^T rows of 64 slots (128 bytes)
+  static constexpr int V_BYTES = BN * KROW;
   static constexpr int POS_BYTES = BN * 8;
-  static constexpr int BUF_BYTES = K_BYTES + VT_BYTES + POS_BYTES;
-  static constexpr int LDS_BYTES = 2 * BUF_BYTES;
-  static constexpr int K_LOADS = K_BYTES / (NTHREADS * 16);  // direct loads per wave
-  static constexpr int KEYS_PER_LOAD = 1024 / KROW;          // keys per wave load
+  static constexpr int STAGE_BYTES = K_BYTES + V_BYTES + POS_BYTES;
+  static constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;
+  static constexpr int KV_LOADS = K_BYTES / (NTHREADS * 16);  // per wave, for K and for V
+  static constexpr int ROWS_PER_LOAD = 1024 / KROW;           // rows one wave load covers
+  static constexpr int LOADS_PER_TILE = 2 * KV_LOADS + 1;     // K, V, positions
+  static_assert(KV_LOADS >= 1, "tile too small for one load per wave");
 };
 
-// K row swizzle: 16-byte group g of key row 'key' lives at group (g ^ swz(key)).
+// K row swizzle: 16-byte group c of row 'key' lives at group (c ^ k_swz(key)).
 template <int D> __device__ __forceinline__ int k_swz(int key) {
   if constexpr (D / 8 >= 16) return key & 15;
   else return (key >> 1) & 7;
 }
-__device__ __forceinline__ int vt_swz(int d) { return (d >> 1) & 7; }
-
-// Slot of key 'key' (0..63) in a V^T row: within each 16-key step, keys
-// a*8 + g*4 + b go to slot g*8 + a*4 + b, which makes the 8 keys a lane of half g needs
-// for one MFMA step contiguous (one 16-byte read).
-__device__ __forceinline__ int vt_slot(int key) {
-  return (key & ~15) | (((key >> 2) & 1) << 3) | (((key >> 3) & 1) << 2) | (key & 3);
+// V row swizzle: 64-byte block b of row 'key' lives at block (b ^ v_swz(key)).
+template <int D> __device__ __forceinline__ int v_swz(int key) {
+  if constexpr (D == 128) return key & 3;
+  else return (key >> 1) & 1;
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           kRsrcFlags);
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource: base, stride 0, num_records = bytes (reads at or past it return 0).
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  i32x4 r;
+  r[0] = (int32_t)(uint32_t)a;
+  r[1] = (int32_t)((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = (int32_t)bytes;
+  r[3] = kRsrcFlags;
+  return r;
 }
 
-// 16 bytes per lane from a buffer straight into LDS at lds_base + lane*16.  Kept out of
-// lambdas: used inside one, the builtin makes the host pass drop the kernel's launch stub.
-__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rs, char* lds_base,
-                                                  uint32_t voffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)lds_base, 16, voffset, 0, 0, 0);
+// LDS byte address of a wave-uniform pointer, in an SGPR (M0 takes scalar operands only)
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_ptr)p);
+}
+
+// Buffer loads straight into LDS (M0 = LDS base, lane l writes base + l*size).  Issued as
+// inline assembly: the kernel waits for them explicitly with vmcnt, and the compiler, which
+// cannot tell which LDS bytes they write, would otherwise drain every load in flight before
+// each LDS read.  A load the compiler does not see can only make its own waits stricter.
+__device__ __forceinline__ void buffer_load_lds16(i32x4 rs, const char* lds_base, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(lds_addr(lds_base)), "v"(voffset), "s"(rs) : "memory", "m0");
+}
+// 4 bytes per lane (exact per-dword range check: a pair of positions that straddles the end
+// of the key block cannot lose its valid half)
+__device__ __forceinline__ void buffer_load_lds4(i32x4 rs, const char* lds_base, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               ::"s"(lds_addr(lds_base)), "v"(voffset), "s"(rs) : "memory", "m0");
+}
+
+// Workgroup barrier that keeps the compiler from moving memory operations across it without
+// forcing outstanding buffer loads to complete (the pipeline waits for them explicitly).
+__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
+
+template <typename F>
+__device__ __forceinline__ F read_tr_frag(const char* a0, const char* a1) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)a0);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)a1);
+  F f;
+  __builtin_memcpy(&f, &lo, 8);
+  __builtin_memcpy((char*)&f + 8, &hi, 8);
+  return f;
 }
 
 __device__ __forceinline__ float max3f(float a, float b, float c) {
   return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
 }
 
-// max of x over the two 32-lane halves of the wave (v_permlane32_swap)
+// max / sum of x over the two 32-lane halves of the wave (v_permlane32_swap)
 __device__ __forceinline__ float max_halves(float x) {
   const uint32_t u = __float_as_uint(x);
   const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
@@ -115,12 +151,22 @@ __device__ __forceinline__ float sum_halves(float x) {
   return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
+// Waits until at most 'ahead' tiles' worth of this wave's buffer loads are outstanding.
+template <int LPT> __device__ __forceinline__ void wait_tiles_ahead(int ahead) {
+  static_assert(NSTAGE == 4, "wait ladder written for 2 tiles ahead at most");
+  if (ahead >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPT) : "memory");
+  else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPT) : "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnParams p) {
   typedef Layout<D> L;
   typedef typename Mfma<T>::frag frag;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  __shared__ int64_t red_q[2][4];
+  __shared__ int tile_list[LIST_CAP];
+  __shared__ int64_t red_q[NWAVES];
+  __shared__ int wave_cnt[NWAVES];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -148,12 +194,11 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   const int64_t qmin_w = wave_min_i64(row_ok ? qpos : INT64_MAX);
   const int64_t qmax_w = wave_max_i64(row_ok ? qpos : INT64_MIN);
   const bool wave_active = __builtin_amdgcn_readfirstlane(qb * BM + wave * 32 < p.Sq ? 1 : 0);
-  if (lane == 0) {
-    red_q[0][wave] = qmin_w;
-    red_q[1][wave] = qmax_w;
-  }
+  if (lane == 0) red_q[wave] = qmax_w;
   __syncthreads();
-  const int64_t qmax_wg = max(max(red_q[1][0], red_q[1][1]), max(red_q[1][2], red_q[1][3]));
+  int64_t qmax_wg = red_q[0];
+#pragma unroll
+  for (int w = 1; w < NWAVES; ++w) qmax_wg = max(qmax_wg, red_q[w]);
 
   // ---- scale folded into exp2: p = exp2(s*c - m*c), c = |scale|*log2(e) > 0.  A negative
   // scale is absorbed by negating Q (exact in bf16/f16).
@@ -176,97 +221,52 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
 
   const char* kbase = (const char*)((const T*)p.k + b * p.ks_b + kvh * p.ks_h);
   const char* vbase = (const char*)((const T*)p.v + b * p.vs_b + kvh * p.vs_h);
-  const int64_t* kpos_b = p.k_pos + b * p.kps_b;
+  const char* pbase = (const char*)(p.k_pos + b * p.kps_b);
   const TileInfo* tinfo = p.tiles + (int64_t)b * p.ntiles;
   const uint32_t krow_bytes = (uint32_t)(p.ks_s * 2), vrow_bytes = (uint32_t)(p.vs_s * 2);
 
-  // ---- per-lane constant offsets
-  // direct K loads: wave load i covers keys (wave*K_LOADS+i)*KEYS_PER_LOAD ...; lane l writes
-  // LDS bytes l*16 of that 1 KB and so must fetch logical group (l % NCG) ^ swz(key)
-  uint32_t k_voff[L::K_LOADS];
+  // ---- per-lane constant offsets of the direct loads: wave load i covers rows
+  // (wave*KV_LOADS + i)*ROWS_PER_LOAD ...; lane l lands on LDS bytes l*16 of that 1 KB and
+  // fetches the logical 16-byte group the swizzle puts there
+  uint32_t k_voff[L::KV_LOADS], v_voff[L::KV_LOADS];
 #pragma unroll
-  for (int i = 0; i < L::K_LOADS; ++i) {
-    const int key = (wave * L::K_LOADS + i) * L::KEYS_PER_LOAD + lane / L::NCG;
-    const int cg = (lane % L::NCG) ^ k_swz<D>(key);
-    k_voff[i] = key * krow_bytes + cg * 16;
+  for (int i = 0; i < L::KV_LOADS; ++i) {
+    const int key = (wave * L::KV_LOADS + i) * L::ROWS_PER_LOAD + lane / L::NCG;
+    const int pg = lane % L::NCG;  // physical 16-byte group in the row
+    k_voff[i] = key * krow_bytes + ((pg ^ k_swz<D>(key)) << 4);
+    const int lgv = (((pg >> 2) ^ v_swz<D>(key)) << 2) | (pg & 3);
+    v_voff[i] = key * vrow_bytes + (lgv << 4);
   }
-  // V: lane owns 4 consecutive keys x 8 features; transposed LDS writes
-  const int v_kq = (lane >> 1) & 15;
-  const int v_c = (lane & 1) + 2 * (lane >> 5) + 4 * wave;  // 8-feature chunk of V
-  const bool v_on = v_c < D / 8;
-  uint32_t v_voff[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) v_voff[j] = (v_kq * 4 + j) * vrow_bytes + v_c * 16;
-  uint32_t v_waddr[8];
-  {
-    const int slot = vt_slot(v_kq * 4);
-    const int cgv = slot >> 3, within = (slot & 7) * 2;
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-      const int d = v_c * 8 + (dd ^ (v_c & 1));  // alternate row order between lane pairs
-      v_waddr[dd] = L::K_BYTES + d * 128 + ((cgv ^ vt_swz(d)) << 4) + within;
-    }
-  }
-  // fragment reads
+  const uint32_t p_voff = wave * 64 + (lane & 15) * 4;  // 8 positions per wave, 16 lanes x 4 B
+
+  // fragment reads: K rows for S^T, transposing reads for V^T
   uint32_t k_raddr[D / 16];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks) k_raddr[ks] = r * L::KROW + (((2 * ks + g) ^ k_swz<D>(r)) << 4);
-  uint32_t v_raddr[4];
+  uint32_t v_raddr[D / 32];
+  {
+    const int src = lane & 15, grp = lane >> 4;
+    const int vrow = g * 4 + (src >> 2);  // + s*16 + half*8 (immediates), multiple-of-4 base
 #pragma unroll
-  for (int s = 0; s < 4; ++s) v_raddr[s] = L::K_BYTES + r * 128 + (((2 * s + g) ^ vt_swz(r)) << 4);
+    for (int dt = 0; dt < D / 32; ++dt)
+      v_raddr[dt] = L::K_BYTES + vrow * L::KROW + ((dt ^ v_swz<D>(vrow)) << 6) +
+                    (16 * (grp & 1) + 4 * (src & 3)) * 2;
+  }
 
-  // ---- list of tiles the workgroup visits: 64 summaries per ballot
-  int chunk_base = -64;
-  uint64_t chunk_mask = 0;
-  auto next_tile = [&]() -> int {
-    while (chunk_mask == 0) {
-      chunk_base += 64;
-      if (chunk_base >= p.ntiles) return -1;
-      const int t = chunk_base + lane;
-      bool need = false;
-      if (t < p.ntiles) {
-        const TileInfo ti = tinfo[t];
-        need = ti.n_valid > 0 && !(p.causal && qmax_wg < ti.min_valid);
-      }
-      chunk_mask = __ballot(need);
-    }
-    const int t = chunk_base + __builtin_ctzll(chunk_mask);
-    chunk_mask &= chunk_mask - 1;
-    return __builtin_amdgcn_readfirstlane(t);
-  };
-
-  u32x4 vreg[4];
-  int64_t preg = -1;
-  // issue the global reads of tile t: K straight into LDS buffer 'bo', V and positions to VGPRs
-  auto load_tile = [&](int t, int bo) {
+  auto load_tile = [&](int t, int stage) {
     const int key0 = t * BN;
-    const int left = p.Sk - key0;  // > 0 for every visited tile
-    const uint32_t kbytes = (uint32_t)(left - 1) * krow_bytes + L::KROW;
-    const uint32_t vbytes = (uint32_t)(left - 1) * vrow_bytes + L::KROW;
-    const auto krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, kbytes);
-    const auto vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, vbytes);
+    const int left = p.Sk - key0;  // > 0 for every listed tile
+    const auto krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, (uint32_t)(left - 1) * krow_bytes + L::KROW);
+    const auto vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, (uint32_t)(left - 1) * vrow_bytes + L::KROW);
+    char* st = smem + stage * L::STAGE_BYTES;
 #pragma unroll
-    for (int i = 0; i < L::K_LOADS; ++i)
-      buffer_load_lds16(krs, smem + bo + (wave * L::K_LOADS + i) * 1024, k_voff[i]);
+    for (int i = 0; i < L::KV_LOADS; ++i)
+      buffer_load_lds16(krs, st + (wave * L::KV_LOADS + i) * 1024, k_voff[i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      vreg[j] = v_on ? __builtin_amdgcn_raw_buffer_load_b128(vrs, v_voff[j], 0, 0) : u32x4{0, 0, 0, 0};
-    if (tid < BN) preg = tid < left ? kpos_b[(int64_t)(key0 + tid) * p.kps_s] : -1;
-  };
-  // write the register-staged part of a tile (V^T, positions) into LDS buffer 'bo'
-  auto store_tile = [&](int bo) {
-    if (v_on) {
-#pragma unroll
-      for (int dd = 0; dd < 8; ++dd) {
-        const int e = dd ^ (v_c & 1);
-        const int wi = e >> 1;
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t lo = __builtin_amdgcn_perm(vreg[1][wi], vreg[0][wi], sel);
-        const uint32_t hi = __builtin_amdgcn_perm(vreg[3][wi], vreg[2][wi], sel);
-        *(u32x2*)(smem + bo + v_waddr[dd]) = u32x2{lo, hi};
-      }
-    }
-    if (tid < BN) *(int64_t*)(smem + bo + L::K_BYTES + L::VT_BYTES + tid * 8) = preg;
+    for (int i = 0; i < L::KV_LOADS; ++i)
+      buffer_load_lds16(vrs, st + L::K_BYTES + (wave * L::KV_LOADS + i) * 1024, v_voff[i]);
+    const auto prs = make_rsrc(pbase + (int64_t)key0 * 8, (uint32_t)left * 8);
+    if (lane < 16) buffer_load_lds4(prs, st + L::K_BYTES + L::V_BYTES + wave * 64, p_voff);
   };
 
   f32x16 oacc[D / 32];
@@ -278,15 +278,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   float m_use = 0.f;                // m_run * c, or 0 while the row has seen nothing
   float l_run = 0.f;                // this lane's partial row sum
 
-  auto compute = [&](auto bufc, int t) {
-    constexpr int BO = decltype(bufc)::value * L::BUF_BYTES;
-    const TileInfo ti = tinfo[t];
+  // per-tile summaries are read through the constant address space: scalar loads, counted
+  // by lgkmcnt, so reading one does not wait for the tile loads in flight (vmcnt)
+  typedef const __attribute__((address_space(4))) TileInfo* tinfo_const_ptr;
+  const tinfo_const_ptr tinfo_c = (tinfo_const_ptr)tinfo;
+
+  auto compute = [&](int stage, int t) {
+    const int n_valid = tinfo_c[t].n_valid;
+    const int64_t min_valid = tinfo_c[t].min_valid, max_valid = tinfo_c[t].max_valid;
     int mode;  // 0 skip, 1 full, 2 element-masked
-    if (!wave_active || ti.n_valid == 0 || (p.causal && qmax_w < ti.min_valid)) mode = 0;
-    else if (ti.n_valid == BN && (!p.causal || ti.max_valid <= qmin_w)) mode = 1;
+    if (!wave_active || n_valid == 0 || (p.causal && qmax_w < min_valid)) mode = 0;
+    else if (n_valid == BN && (!p.causal || max_valid <= qmin_w)) mode = 1;
     else mode = 2;
     mode = __builtin_amdgcn_readfirstlane(mode);
     if (mode == 0) return;
+    const char* sb = smem + stage * L::STAGE_BYTES;
 
     f32x16 sacc[2];
 #pragma unroll
@@ -294,22 +300,24 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
       frag kf[D / 16];
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks)
-        kf[ks] = *(const frag*)(smem + BO + kb * 32 * L::KROW + k_raddr[ks]);
+        kf[ks] = *(const frag*)(sb + kb * 32 * L::KROW + k_raddr[ks]);
       f32x16 acc = {};
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) acc = Mfma<T>::run(kf[ks], qf[ks], acc);
       sacc[kb] = acc;
     }
     if (mode == 2) {
-      const char* pl = smem + BO + L::K_BYTES + L::VT_BYTES + g * 32;
+      const char* pl = sb + L::K_BYTES + L::V_BYTES;
+      const int left = p.Sk - t * BN;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int64_t kp = *(const int64_t*)(pl + (kb * 32 + i4 * 8 + j) * 8);
-            const bool vis = row_ok && kp >= 0 && (!p.causal || kp <= qpos);
+            const int key = kb * 32 + i4 * 8 + g * 4 + j;
+            const int64_t kp = *(const int64_t*)(pl + key * 8);
+            const bool vis = row_ok && key < left && kp >= 0 && (!p.causal || kp <= qpos);
             if (!vis) sacc[kb][i4 * 4 + j] = -__builtin_inff();
           }
         }
@@ -346,46 +354,55 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
         pf[kb * 2 + (e >> 3)][e & 7] = (T)pv;
       }
     l_run += psum;
-    // O^T += V^T . P^T
+    // O^T += V^T . P^T: fragment of step s holds keys s*16 + {g*4..+3, 8+g*4..+3}
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
       frag vf[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) vf[s] = *(const frag*)(smem + BO + dt * 32 * 128 + v_raddr[s]);
+      for (int s = 0; s < 4; ++s)
+        vf[s] = read_tr_frag<frag>(sb + s * 16 * L::KROW + v_raddr[dt],
+                                   sb + (s * 16 + 8) * L::KROW + v_raddr[dt]);
 #pragma unroll
       for (int s = 0; s < 4; ++s) oacc[dt] = Mfma<T>::run(vf[s], pf[s], oacc[dt]);
     }
   };
 
-  auto sync_tile = [&]() {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  };
-
-  int t_cur = next_tile();
-  if (t_cur >= 0) {
-    load_tile(t_cur, 0);
-    store_tile(0);
-  }
-  sync_tile();
-  // two-stage software pipeline, unrolled so each stage reads one LDS buffer with
-  // immediate offsets: buffer 0 holds t_cur on entry of the first stage
-  while (t_cur >= 0) {
-    int t_next = next_tile();
-    if (t_next >= 0) load_tile(t_next, L::BUF_BYTES);
-    compute(std::integral_constant<int, 0>(), t_cur);
-    if (t_next < 0) break;
-    store_tile(L::BUF_BYTES);
-    sync_tile();
-    t_cur = t_next;
-
-    t_next = next_tile();
-    if (t_next >= 0) load_tile(t_next, 0);
-    compute(std::integral_constant<int, 1>(), t_cur);
-    if (t_next < 0) break;
-    store_tile(0);
-    sync_tile();
-    t_cur = t_next;
+  // ---- passes over the key block: list the tiles this workgroup needs, then stream them
+  for (int base = 0; base < p.ntiles; base += LIST_CAP) {
+    const int span = min(LIST_CAP, p.ntiles - base);
+    int n = 0;
+    for (int r0 = 0; r0 < span; r0 += NTHREADS) {
+      const int t = base + r0 + tid;
+      bool need = false;
+      if (r0 + tid < span) {
+        const TileInfo ti = tinfo[t];
+        need = ti.n_valid > 0 && !(p.causal && qmax_wg < ti.min_valid);
+      }
+      const uint64_t bal = __ballot(need);
+      if (lane == 0) wave_cnt[wave] = __builtin_popcountll(bal);
+      __syncthreads();
+      int off = n;
+      for (int w = 0; w < wave; ++w) off += wave_cnt[w];
+      int tot = n;
+      for (int w = 0; w < NWAVES; ++w) tot += wave_cnt[w];
+      if (need) tile_list[off + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0))] = t;
+      __syncthreads();
+      n = tot;
+    }
+    if (n == 0) continue;
+    int issued = 0;
+    for (; issued < n && issued < NSTAGE - 1; ++issued) load_tile(tile_list[issued], issued % NSTAGE);
+    for (int i = 0; i < n; ++i) {
+      wait_tiles_ahead<L::LOADS_PER_TILE>(issued - i - 1);
+      barrier_no_fence();  // tile i landed for every wave; the stage of tile i-1 is free
+      if (issued < n) {
+        load_tile(tile_list[issued], issued % NSTAGE);
+        ++issued;
+      }
+      compute(i % NSTAGE, __builtin_amdgcn_readfirstlane(tile_list[i]));
+    }
+    __syncthreads();  // the next pass rewrites the list and the stages
   }
 
   // ---- epilogue: normalise, emit (out, lse) or merge them into the running pair
@@ -488,6 +505,8 @@ bool prefill_mfma_supported(const AttnParams& p) {
   const int64_t so[] = {p.os_b, p.os_s, p.os_h};
   for (int64_t s : so)
     if (s % 4) return false;
+  // key positions are fetched 16 bytes at a time: contiguous, 16-byte aligned per batch
+  if (p.kps_s != 1 || p.kps_b % 2 || !al16(p.k_pos)) return false;
   // buffer resources address one (batch, kv head) block with 32-bit offsets: rows must not
   // overlap and the block must stay below 2 GiB
   if (p.ks_s < p.D || p.vs_s < p.D) return false;

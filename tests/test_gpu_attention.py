@@ -37,6 +37,13 @@ CASES = [
     Case(1, 100, 100, 2, 2, 64, "aligned", True, scale=0.0),
     Case(1, 33, 65, 2, 1, 128, "all_pad", True),
     Case(1, 257, 257, 2, 1, 96, "aligned", True),
+    # odd key counts (partial last tile), pipelines of many tiles, several list passes
+    Case(2, 97, 131, 8, 2, 128, "random", True),
+    Case(1, 131, 131, 4, 1, 128, "left_pad", True),
+    Case(1, 257, 257, 8, 8, 64, "aligned", True),
+    Case(1, 700, 700, 2, 1, 128, "aligned", True),
+    Case(2, 300, 777, 4, 2, 128, "random", False),
+    Case(1, 2, 140001, 2, 1, 64, "decode", True),
 ]
 
 DTYPES = [torch.float64, torch.float32, torch.bfloat16, torch.float16]
