@@ -141,8 +141,91 @@ static int make_attn_params(AttnParams* p, const cea_tensor* q, const cea_tensor
   return CEA_OK;
 }
 
+// Split-KV decode over n KV blocks that share q / q_pos / out (n = 1: one attention call).
+struct DecodePlan {
+  int chunk;
+  int total_chunks;
+  int nr;
+  size_t partial_bytes;
+};
+
+static DecodePlan plan_decode(const int64_t* Sk, int n, int64_t B, int64_t Sq, int64_t Hq,
+                              int64_t Hkv, int64_t D) {
+  DecodePlan pl;
+  int64_t keys = 0;
+  for (int i = 0; i < n; ++i) keys += Sk[i];
+  pl.chunk = decode_plan_chunk(keys, (int32_t)B, (int32_t)Hkv);
+  pl.total_chunks = 0;
+  for (int i = 0; i < n; ++i) pl.total_chunks += (int)((Sk[i] + pl.chunk - 1) / pl.chunk);
+  pl.nr = decode_rows((int32_t)Sq, (int32_t)(Hq / (Hkv > 0 ? Hkv : 1)));
+  pl.partial_bytes = align_up((size_t)(B * Hkv) * pl.total_chunks * (pl.nr > 0 ? pl.nr : 1) *
+                                  (D + 2) * sizeof(float), 256);
+  return pl;
+}
+
+// Fills a DecodeParams from n per-block parameter blocks (same q, q_pos, out, lse).
+static int run_decode(const AttnParams* blocks, int n, cea_tensor* part_out, cea_tensor* part_lse,
+                      char* ws, size_t ws_bytes, hipStream_t st) {
+  const AttnParams& a = blocks[0];
+  int64_t sks[CEA_MAX_PARTS];
+  for (int i = 0; i < n; ++i) sks[i] = blocks[i].Sk;
+  const DecodePlan pl = plan_decode(sks, n, a.B, a.Sq, a.Hq, a.Hkv, a.D);
+  CEA_REQUIRE(ws != nullptr && ws_bytes >= pl.partial_bytes, CEA_ENOSPACE,
+              "decode: workspace of %zu bytes needed, %zu given", pl.partial_bytes, ws_bytes);
+  DecodeParams d;
+  memset(&d, 0, sizeof(d));
+  d.nparts = n;
+  d.q = a.q; d.q_pos = a.q_pos;
+  d.B = a.B; d.Sq = a.Sq; d.Hq = a.Hq; d.Hkv = a.Hkv; d.D = a.D;
+  d.qs_b = a.qs_b; d.qs_s = a.qs_s; d.qs_h = a.qs_h;
+  d.qps_b = a.qps_b; d.qps_s = a.qps_s;
+  d.chunk = pl.chunk;
+  d.chunk_begin[0] = 0;
+  for (int i = 0; i < n; ++i) {
+    const AttnParams& bi = blocks[i];
+    d.k[i] = bi.k; d.v[i] = bi.v; d.k_pos[i] = bi.k_pos;
+    d.Sk[i] = bi.Sk;
+    d.ks[i][0] = bi.ks_b; d.ks[i][1] = bi.ks_s; d.ks[i][2] = bi.ks_h;
+    d.vs[i][0] = bi.vs_b; d.vs[i][1] = bi.vs_s; d.vs[i][2] = bi.vs_h;
+    d.kps[i][0] = bi.kps_b; d.kps[i][1] = bi.kps_s;
+    d.chunk_begin[i + 1] = d.chunk_begin[i] + (bi.Sk + pl.chunk - 1) / pl.chunk;
+    if (part_out) {
+      d.part_out[i] = part_out[i].data;
+      d.part_lse[i] = part_lse[i].data;
+      for (int j = 0; j < 3; ++j) {
+        d.pos_[i][j] = part_out[i].stride[j];
+        d.pls_[i][j] = part_lse[i].stride[j];
+      }
+    }
+  }
+  d.scale = a.scale;
+  d.causal = a.causal;
+  d.in_dtype = a.in_dtype;
+  d.map = a.map;
+  d.partial = (float*)ws;
+  d.G = a.Hq / a.Hkv;
+  d.out = a.out; d.lse = a.lse;
+  d.os_b = a.os_b; d.os_s = a.os_s; d.os_h = a.os_h;
+  d.ls_b = a.ls_b; d.ls_h = a.ls_h; d.ls_s = a.ls_s;
+  d.out_dtype = a.out_dtype;
+  d.accumulate = a.accumulate;
+  return launch_attn_decode(d, st);
+}
+
+static bool use_decode(const AttnParams& p) {
+  if (!decode_supported(p.Sq, p.Hq, p.Hkv, p.D, p.in_dtype, p.map)) return false;
+  if (!(p.out_dtype == CEA_F32 || p.out_dtype == p.in_dtype)) return false;
+  if (p.accumulate && p.out_dtype != CEA_F32) return false;
+  if (!(fabs(p.scale) >= 1e-30 && fabs(p.scale) <= 1e30)) return false;
+  const int64_t s8[] = {p.qs_b, p.qs_s, p.qs_h, p.ks_b, p.ks_s, p.ks_h, p.vs_b, p.vs_s, p.vs_h};
+  for (int64_t s : s8)
+    if (s % 8) return false;
+  return ((uintptr_t)p.q & 15) == 0 && ((uintptr_t)p.k & 15) == 0 && ((uintptr_t)p.v & 15) == 0;
+}
+
 // Runs one attention call with a prepared parameter block.
 static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t st) {
+  if (p.Sk > 0 && use_decode(p)) return run_decode(&p, 1, nullptr, nullptr, ws, ws_bytes, st);
   if (p.Sk > 0 && prefill_mfma_supported(p)) {
     const size_t need = tile_bytes(p.B, p.Sk);
     CEA_REQUIRE(ws != nullptr && ws_bytes >= need, CEA_ENOSPACE,
@@ -167,9 +250,14 @@ int cea_version(void) { return 100; }
 
 size_t cea_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int64_t Hkv,
                                      int64_t D, int32_t in_dtype) {
-  (void)Sq; (void)Hq; (void)Hkv; (void)D; (void)in_dtype;
+  (void)in_dtype;
   if (B <= 0 || Sk <= 0) return 256;
-  return tile_bytes(B, Sk);
+  size_t need = tile_bytes(B, Sk);
+  if (Hkv > 0 && Hq % Hkv == 0 && decode_rows((int32_t)Sq, (int32_t)(Hq / Hkv)) > 0) {
+    const size_t dec = plan_decode(&Sk, 1, B, Sq, Hq, Hkv, D).partial_bytes;
+    need = dec > need ? dec : need;
+  }
+  return need;
 }
 
 int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
@@ -268,6 +356,10 @@ size_t cea_partitioned_attention_workspace_bytes(int32_t n, const int64_t* Sk, i
   // per-partition partials (out, lse) in the accumulation dtype
   need += (size_t)n * align_up((size_t)(B * Sq * Hq * D) * esz, 256);
   need += (size_t)n * align_up((size_t)(B * Hq * Sq) * esz, 256);
+  if (Hkv > 0 && Hq % Hkv == 0 && decode_rows((int32_t)Sq, (int32_t)(Hq / Hkv)) > 0) {
+    const size_t dec = plan_decode(Sk, n, B, Sq, Hq, Hkv, D).partial_bytes;
+    need = dec > need ? dec : need;
+  }
   return need;
 }
 
@@ -300,6 +392,31 @@ int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* 
               "partitioned attention: workspace of %zu bytes needed, %zu given", need,
               workspace_bytes);
   char* ws = (char*)workspace;
+  // fast path: every partition through the split-KV decode kernels, merged in one reduction
+  {
+    AttnParams blocks[CEA_MAX_PARTS];
+    bool dec = true;
+    for (int i = 0; i < n; ++i) {
+      rc = make_attn_params(&blocks[i], q, &ks[i], &vs[i], q_pos, &k_pos_s[i], causal, scale,
+                            kv_map, kv_map_len, out, lse, 0);
+      if (rc) return rc;
+      dec = dec && use_decode(blocks[i]);
+    }
+    if (dec && part_out) {
+      for (int i = 0; i < n && rc == 0; ++i) {
+        rc = check_tensor(&part_out[i], "part_out", 4, acc, true);
+        if (!rc) rc = check_tensor(&part_lse[i], "part_lse", 3, acc, false);
+        if (!rc)
+          CEA_REQUIRE(part_out[i].size[0] == B && part_out[i].size[1] == Sq &&
+                          part_out[i].size[2] == Hq && part_out[i].size[3] == D &&
+                          part_lse[i].size[0] == B && part_lse[i].size[1] == Hq &&
+                          part_lse[i].size[2] == Sq,
+                      CEA_EINVAL, "partitioned attention: per-partition outputs have wrong shapes");
+      }
+      if (rc) return rc;
+    }
+    if (dec) return run_decode(blocks, n, part_out, part_lse, ws, workspace_bytes, st);
+  }
   int64_t maxsk = 0;
   for (int i = 0; i < n; ++i) maxsk = sks[i] > maxsk ? sks[i] : maxsk;
   char* tiles = ws;

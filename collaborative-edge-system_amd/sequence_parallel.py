@@ -191,7 +191,9 @@ def partitioned_attention(
         _check_heads(q.shape[2], kk.shape[2], mapping)
     B, Sq, Hq, D = q.shape
     acc = accumulation_dtype(q.dtype)
-    out = torch.empty(B, Sq, Hq, D, dtype=out_dtype or q.dtype, device=q.device)
+    if out_dtype is None:  # the merged lse comes with an accumulation-precision output
+        out_dtype = acc if return_lse else q.dtype
+    out = torch.empty(B, Sq, Hq, D, dtype=out_dtype, device=q.device)
     lse = torch.empty(B, Hq, Sq, dtype=acc, device=q.device) if return_lse else None
     lib = nat.load_library()
     n = len(parts)

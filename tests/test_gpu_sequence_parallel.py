@@ -1,0 +1,147 @@
+"""GPU parity of the per-rank sequence-parallel shares and the split-KV decode path.
+
+* ring / Ulysses / distributed-KV on simulated ranks == single-device attention, in f64
+  (tests/test_sequence_parallel.py:15-67 of the reference, err < 1e-12 there; 1e-10 here)
+  and against the CPU oracle of the same shares in bf16;
+* the split-KV decode kernels (short query blocks, cache views, partitions) against the
+  oracle's per-partition attention and merge, including each partition's (out, lse).
+Tolerances as stated in tests/_cases.py.
+"""
+
+import pytest
+import torch
+
+from _cases import Case, assert_attention_close, make_positions
+from oracle import attention_ref as ref
+from oracle import sp_ref
+
+pytestmark = pytest.mark.gpu
+
+B, S, HQ, HKV, D = 2, 13, 6, 3, 4
+
+
+def _inputs(dtype=torch.float64, d=D, hq=HQ, hkv=HKV, s=S, b=B):
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(b, s, hq, d, generator=g, dtype=torch.float64).to(dtype)
+    k = torch.randn(b, s, hkv, d, generator=g, dtype=torch.float64).to(dtype)
+    v = torch.randn(b, s, hkv, d, generator=g, dtype=torch.float64).to(dtype)
+    pos = torch.arange(s).repeat(b, 1)
+    pos[1, :3] = -1  # left padding in the second sequence
+    pos[1, 3:] -= 3
+    return q, k, v, pos
+
+
+@pytest.mark.parametrize(
+    "world,kind,weights,causal",
+    [(2, "contiguous", None, True), (2, "zigzag", None, True), (3, "zigzag", [3, 2, 1], True),
+     (3, "contiguous", [1, 2, 3], False)],
+)
+def test_shares_match_single_device_f64(cea, dev, world, kind, weights, causal):
+    q, k, v, pos = (t.to(dev) for t in _inputs())
+    full = cea.attention.attention(q, k, v, pos, pos, causal=causal)
+    valid = (pos >= 0).cpu()
+    layout = cea.SequenceLayout(S, world, weights, kind)
+    group = cea.LocalGroup(world)
+    for r in range(world):
+        group.set_shard(r, q=layout.shard(q, r), k=layout.shard(k, r), v=layout.shard(v, r),
+                        pos=layout.shard(pos, r))
+    ring_parts, uly_parts = [], []
+    shards = cea.partition_heads(HQ, HKV, weights or world)
+    for r in range(world):
+        me = group.view_as(r)
+        sh = group.shard(r)
+        ring_parts.append(cea.ring_attention(sh["q"], sh["k"], sh["v"], sh["pos"], sh["pos"], me,
+                                             layout.sizes, causal=causal))
+        out, _ = cea.ulysses_attention(sh["q"], sh["k"], sh["v"], sh["pos"], me, layout.sizes,
+                                       shards, causal=causal)
+        uly_parts.append(out)
+    torch.cuda.synchronize()
+    ring = layout.unshard(ring_parts).cpu()
+    uly = layout.unshard(uly_parts).cpu()
+    assert (ring - full.cpu())[valid].abs().max().item() < 1e-10
+    assert (uly - full.cpu())[valid].abs().max().item() < 1e-10
+    # decoding: the last two tokens against the sequence-sharded cache
+    dkv = cea.distributed_kv_attention(q[:, -2:], group.shard(0)["k"], group.shard(0)["v"],
+                                       pos[:, -2:], group.shard(0)["pos"], group, causal=causal)
+    torch.cuda.synchronize()
+    assert (dkv.cpu() - full.cpu()[:, -2:]).abs().max().item() < 1e-10
+
+
+def test_ring_share_bf16_matches_oracle(cea, dev):
+    """A small zigzag ring share in bf16 against the oracle's ring loop (skip rule, order)."""
+    w = cea.workloads.ring_share(seq_len=2048, sp=4, rank=1, hq=8, hkv=2, d=128)
+    blocks = [(k.to(dev), v.to(dev), p.to(dev)) for k, v, p in w.blocks]
+    group = cea.LocalGroup(4, 1)
+    for r, (k, v, p) in enumerate(blocks):
+        group.set_shard(r, k=k, v=v, pos=p)
+    k1, v1, p1 = blocks[1]
+    out, lse = cea.sequence_parallel.ring_attention_with_lse(
+        w.q.to(dev), k1, v1, w.q_pos.to(dev), p1, group, w.kv_sizes)
+    ro, rl = sp_ref.ring_share(w.q, w.q_pos, w.blocks, 1, with_lse=True)
+    torch.cuda.synchronize()
+    assert_attention_close(out, lse, ro, rl, torch.bfloat16, "ring share")
+
+
+DECODE_CASES = [
+    # (B, Sq, Hq, Hkv, cap, parts)
+    (3, 1, 32, 8, 700, [400, 300]),
+    (2, 1, 8, 8, 1500, [1500]),
+    (2, 2, 8, 4, 999, [333, 333, 333]),
+    (2, 4, 4, 4, 513, [100, 13, 400]),
+    (1, 1, 16, 4, 5000, [2000, 1500, 1000, 500]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
+@pytest.mark.parametrize("shape", DECODE_CASES, ids=lambda s: "B{}-Sq{}-H{}/{}-cap{}-p{}".format(*s[:5], len(s[5])))
+def test_partitioned_decode_matches_oracle(cea, dev, shape, dtype):
+    Bn, Sq, Hq, Hkv, cap, sizes = shape
+    g = torch.Generator().manual_seed(sum(sizes) + Sq)
+    ck = torch.randn(Bn, Hkv, cap, 128, generator=g).to(dtype)
+    cv = torch.randn(Bn, Hkv, cap, 128, generator=g).to(dtype)
+    q = torch.randn(Bn, Sq, Hq, 128, generator=g).to(dtype)
+    lens = torch.randint(1, cap + 1, (Bn,), generator=g)
+    slots = torch.arange(cap).view(1, cap)
+    kpos = torch.where(slots < lens.view(-1, 1), slots, torch.full_like(slots, -1))
+    qpos = (lens - 1).view(-1, 1) + torch.arange(Sq).view(1, Sq) - (Sq - 1)
+    qpos = qpos.clamp(min=0)
+    ckd, cvd, kpd = ck.to(dev), cv.to(dev), kpos.to(dev)
+    parts, parts_cpu, start = [], [], 0
+    for n in sizes:
+        parts.append((ckd[:, :, start:start + n].transpose(1, 2), cvd[:, :, start:start + n].transpose(1, 2),
+                      kpd[:, start:start + n]))
+        parts_cpu.append((ck[:, :, start:start + n].transpose(1, 2), cv[:, :, start:start + n].transpose(1, 2),
+                          kpos[:, start:start + n]))
+        start += n
+    out, lse, per = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts, return_lse=True,
+                                              return_parts=True)
+    out_q = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts)
+    ro, rl, rparts = sp_ref.distributed_kv_share(q, qpos, parts_cpu, with_parts=True)
+    torch.cuda.synchronize()
+    assert out_q.dtype == dtype
+    for (po, pl), (qo, ql) in zip(per, rparts):
+        assert_attention_close(po, pl, qo, ql, dtype, "partition")
+    assert_attention_close(out, lse, ro.float(), rl, dtype, "merged")
+    assert (out_q.cpu().float() - ro.float()).abs().max().item() <= 2e-2
+    # single-partition attention_with_lse on the decode path (and its kv_block variant)
+    o1, l1 = cea.attention_with_lse(q.to(dev), *parts[0][:2], qpos.to(dev), parts[0][2])
+    r1, s1 = ref.attention_with_lse(q, *parts_cpu[0][:2], qpos, parts_cpu[0][2])
+    torch.cuda.synchronize()
+    assert_attention_close(o1, l1, r1, s1, dtype, "single partition")
+
+
+def test_kv_decode_workload_subset_matches_oracle(cea, dev):
+    """Four sequences of the distributed-KV decode workload (cache 32768, 4 partitions)
+    through distributed_kv_attention on simulated ranks vs the oracle."""
+    w = cea.workloads.kv_decode(device=dev, batch=[0, 7, 19, 31])
+    wc = cea.workloads.kv_decode(device="cpu", batch=[0, 7, 19, 31])
+    parts = w.partitions()
+    group = cea.LocalGroup(len(parts))
+    for r, (k, v, p) in enumerate(parts):
+        group.set_shard(r, k=k, v=v, pos=p)
+    out = cea.distributed_kv_attention(w.q, parts[0][0], parts[0][1], w.q_pos, parts[0][2], group)
+    ro = sp_ref.distributed_kv_share(wc.q, wc.q_pos, wc.partitions())
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16
+    err = (out.cpu().float() - ro.float()).abs().max().item()
+    assert err <= 2e-2, err
