@@ -193,7 +193,19 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,ulysses,f32")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="only run a device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
+    if args.calib_copy:
+        import torch
+
+        n = args.calib_copy * (1 << 20) // 4
+        src = torch.randn(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        sec = _timed(lambda: dst.copy_(src), 10, 2, torch)
+        print(json.dumps({"calib_copy_mib": args.calib_copy, "read_bytes": n * 4, "write_bytes": n * 4,
+                          "gbs": round(2 * n * 4 / sec / 1e9, 1)}), flush=True)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build simulates every rank's share on a single "
               "MI355X and has no multi-GPU path (run with --gpus 1)", file=sys.stderr)

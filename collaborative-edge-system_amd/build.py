@@ -46,6 +46,7 @@ COMMON_FLAGS = [
 FILE_FLAGS = {
     # M0 is set by the kernel's own LDS-DMA assembly; the clobber note is expected
     "attn_prefill.hip": ["-fno-honor-nans", "-Wno-inline-asm"],
+    "attn_decode.hip": ["-fno-honor-nans", "-Wno-inline-asm"],
 }
 
 

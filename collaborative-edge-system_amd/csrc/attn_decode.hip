@@ -8,69 +8,96 @@
 //
 // HBM-bound design:
 //   * work item = (batch, kv head, key chunk of one partition); the NR = Sq*G query rows that
-//     share the kv head (G query heads per kv head) are processed together, so each K/V row
-//     is read from HBM once for all of them;
-//   * a 16-lane group owns one key row at a time: lane j loads features 8j..8j+7 of K and V
-//     with 16-byte loads (a wave reads 4 consecutive 256-byte rows per instruction);
-//     q.k is 4 v_dot2_f32_bf16 per row plus a 4-step DPP butterfly across the group;
-//   * key positions of the chunk are staged in LDS; keys that no row can see are never
-//     loaded, and chunks past every valid key return after the position scan;
-//   * the 16 groups of a workgroup merge their online-softmax partials in LDS and write one
-//     (o unnormalised, m, l) partial per chunk; the reduction kernel then merges the chunks of
-//     each partition exactly (optionally emitting each partition's (out, lse)), merges the
+//     share the kv head (G query heads per kv head) are the columns of 16 x 16 matrix-core
+//     tiles, so each K/V row is read from HBM once for all of them and the arithmetic stays
+//     off the vector ALU: S = K.Q^T with v_mfma_f32_16x16x32 (a lane holds 4 keys of one
+//     query row) and O^T += V^T.P^T with v_mfma_f32_16x16x16 (P is the score tile as is);
+//   * every wave streams its own 16-key tiles of K and V straight into a private pair of LDS
+//     buffers (buffer_load ... lds, one tile ahead, explicit vmcnt waits, no barriers); V is
+//     read back transposed with ds_read_b64_tr_b16; both tiles are XOR-swizzled so the
+//     fragment and transpose reads are free of LDS bank conflicts;
+//   * key positions of the chunk are staged in LDS; 16-key tiles that no query row can see
+//     are never loaded, and chunks past every valid key return after the position scan;
+//   * the waves of a workgroup merge their online-softmax partials in LDS and write one
+//     (o unnormalised, m, l) partial per chunk; the reduction kernel then merges the chunks
+//     of each partition exactly (optionally emitting each partition's (out, lse)), merges the
 //     partitions with the reference's logsumexp, and writes out (f32 or the query dtype) and
 //     lse.
 #include "cea_kernels.hpp"
+#include "cea_lds_dma.hpp"
 
 namespace cea {
 namespace {
 
 constexpr int DTHREADS = 256;
-constexpr int NGROUPS = DTHREADS / 16;  // 16-lane groups per workgroup
-constexpr int NB = 4;                   // keys per group per batch
-constexpr int BATCH = NGROUPS * NB;     // keys per workgroup batch
+constexpr int NW = DTHREADS / 64;     // waves per workgroup
+constexpr int TK = 16;                // keys per tile
+constexpr int CHMAX = 1024;           // keys per chunk at most
+constexpr int NTILE_MAX = CHMAX / TK;
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold, log2 units
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
-template <typename T> __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c);
-template <> __device__ __forceinline__ float dot2<bf16>(uint32_t a, uint32_t b, float c) {
-  bf16x2 x, y;
-  __builtin_memcpy(&x, &a, 4);
-  __builtin_memcpy(&y, &b, 4);
-  return __builtin_amdgcn_fdot2_f32_bf16(x, y, c, false);
-}
-template <> __device__ __forceinline__ float dot2<f16>(uint32_t a, uint32_t b, float c) {
-  f16x2 x, y;
-  __builtin_memcpy(&x, &a, 4);
-  __builtin_memcpy(&y, &b, 4);
-  return __builtin_amdgcn_fdot2(x, y, c, false);
-}
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16> {
+  typedef bf16x8 frag8;
+  static __device__ __forceinline__ f32x4 qk(frag8 a, frag8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ s16x4 pack(float a, float b, float c, float d) {
+    bf16x4 v = {(bf16)a, (bf16)b, (bf16)c, (bf16)d};
+    s16x4 r;
+    __builtin_memcpy(&r, &v, 8);
+    return r;
+  }
+};
+template <> struct Mfma16<f16> {
+  typedef f16x8 frag8;
+  static __device__ __forceinline__ f32x4 qk(frag8 a, frag8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(s16x4 a, s16x4 b, f32x4 c) {
+    f16x4 x, y;
+    __builtin_memcpy(&x, &a, 8);
+    __builtin_memcpy(&y, &b, 8);
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(x, y, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ s16x4 pack(float a, float b, float c, float d) {
+    f16x4 v = {(f16)a, (f16)b, (f16)c, (f16)d};
+    s16x4 r;
+    __builtin_memcpy(&r, &v, 8);
+    return r;
+  }
+};
 
-template <typename T> __device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi);
-template <> __device__ __forceinline__ void unpack2<bf16>(uint32_t w, float& lo, float& hi) {
-  lo = __uint_as_float(w << 16);
-  hi = __uint_as_float(w & 0xffff0000u);
-}
-template <> __device__ __forceinline__ void unpack2<f16>(uint32_t w, float& lo, float& hi) {
-  f16x2 v;
-  __builtin_memcpy(&v, &w, 4);
-  lo = (float)v[0];
-  hi = (float)v[1];
-}
+template <int D> struct DLayout {
+  static constexpr int ROW = D * 2;                 // bytes per key row
+  static constexpr int TILE_BYTES = TK * ROW;       // one K or V tile
+  static constexpr int BUF_BYTES = 2 * TILE_BYTES;  // K + V
+  static constexpr int WAVE_BYTES = 2 * BUF_BYTES;  // double-buffered per wave
+  static constexpr int LDS_BYTES = NW * WAVE_BYTES;
+  static constexpr int LOADS = TILE_BYTES / 1024;   // direct loads per tensor per tile
+};
 
-// sum over the 16 lanes of a DPP row, result in every lane (xor 1, xor 2, mirror 8, mirror 16)
-__device__ __forceinline__ float row16_sum(float x) {
-  int v = __float_as_int(x);
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
-  v = __float_as_int(x);
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
-  v = __float_as_int(x);
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false)); // row_half_mirror
-  v = __float_as_int(x);
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false)); // row_mirror
-  return x;
+__device__ __forceinline__ float max_halves(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
 __device__ __forceinline__ int part_of(const DecodeParams& p, int chunk) {
@@ -82,13 +109,14 @@ __device__ __forceinline__ int part_of(const DecodeParams& p, int chunk) {
 // Partial layout: [B][Hkv][total_chunks][NR][D + 2] floats: o (relative to m), m, l, where
 // m is in natural-log units (max of scale*q.k) and l = sum exp(scale*q.k - m).
 template <typename T, int D, int NR>
-__global__ __launch_bounds__(DTHREADS) void decode_split_kernel(const DecodeParams p) {
-  constexpr int CHMAX = 2048;
+__global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeParams p) {
+  typedef DLayout<D> L;
+  typedef typename Mfma16<T>::frag8 frag8;
+  extern __shared__ __attribute__((aligned(16))) char dsmem[];
   __shared__ int64_t kpos_s[CHMAX];
-  __shared__ uint32_t batch_any[CHMAX / BATCH];
-  __shared__ float red_m[NGROUPS][NR];
-  __shared__ float red_l[NGROUPS][NR];
-  __shared__ float red_o[NGROUPS][NR][D];
+  __shared__ uint32_t tile_any[NTILE_MAX];
+  __shared__ float red_m[NW][NR];
+  __shared__ float red_l[NW][NR];
 
   const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int part = part_of(p, chunk);
@@ -96,40 +124,42 @@ __global__ __launch_bounds__(DTHREADS) void decode_split_kernel(const DecodePara
   const int Sk = p.Sk[part];
   const int key0 = lchunk * p.chunk;
   const int nkeys = min(p.chunk, Sk - key0);
-  const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 4, li = tid & 15;
+  const int ntile = (nkeys + TK - 1) / TK;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row = lane & 15;   // query row (MFMA column) of this lane
+  const int grp = lane >> 4;   // 4-key group of the 16-key tile
   const int G = p.G;
+  const int nreal = p.Sq * G;
   const int total_chunks = p.chunk_begin[p.nparts];
   float* part_out = p.partial + (((int64_t)b * p.Hkv + kvh) * total_chunks + chunk) * NR * (D + 2);
 
   // ---- query rows of this kv head: row r = (s, gi) -> head kvh*G + gi, position q_pos[b, s]
-  int64_t qp[NR];
+  const bool row_real = row < nreal;
+  const int64_t qpos = row_real ? p.q_pos[b * p.qps_b + (int64_t)(row / G) * p.qps_s] : INT64_MIN;
   int64_t qmax = INT64_MIN;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int s = r / G;
-    qp[r] = (r < p.Sq * G) ? p.q_pos[b * p.qps_b + (int64_t)s * p.qps_s] : INT64_MIN;
-    qmax = qp[r] > qmax ? qp[r] : qmax;
+  for (int r = 0; r < nreal; ++r) {
+    const int64_t v = p.q_pos[b * p.qps_b + (int64_t)(r / G) * p.qps_s];
+    qmax = v > qmax ? v : qmax;
   }
 
-  // ---- positions of the chunk into LDS; which 64-key batches have any visible key
+  // ---- positions of the chunk into LDS; which 16-key tiles have a visible key
   const int64_t* kp = p.k_pos[part] + b * p.kps[part][0];
   const int64_t kps = p.kps[part][1];
   for (int i = tid; i < nkeys; i += DTHREADS) kpos_s[i] = kp[(int64_t)(key0 + i) * kps];
-  const int nbatch = (nkeys + BATCH - 1) / BATCH;
   __syncthreads();
-  for (int bi = tid >> 6; bi < nbatch; bi += DTHREADS / 64) {
-    const int k = bi * BATCH + lane;
+  for (int t0 = wave * 4; t0 < ntile; t0 += NW * 4) {
+    const int k = t0 * TK + lane;
     bool vis = false;
     if (k < nkeys) {
       const int64_t pk = kpos_s[k];
       vis = pk >= 0 && (!p.causal || pk <= qmax);
     }
     const uint64_t bal = __ballot(vis);
-    if (lane == 0) batch_any[bi] = bal != 0;
+    if (lane < 4 && t0 + lane < ntile) tile_any[t0 + lane] = (uint32_t)((bal >> (16 * lane)) & 0xffffu);
   }
   __syncthreads();
   bool any = false;
-  for (int bi = 0; bi < nbatch; ++bi) any |= batch_any[bi] != 0;
+  for (int t = 0; t < ntile; ++t) any |= tile_any[t] != 0;
   if (!any) {
     if (tid < NR) {
       part_out[tid * (D + 2) + D] = -__builtin_inff();
@@ -138,128 +168,167 @@ __global__ __launch_bounds__(DTHREADS) void decode_split_kernel(const DecodePara
     return;
   }
 
-  // ---- this lane's 8 features of every query row (bf16/f16 pairs), sign folded for scale<0
+  // ---- this lane's Q fragments (B operand of S = K.Q^T), sign folded for a negative scale
   const float scale = (float)p.scale;
   const float c = fabsf(scale) * 1.4426950408889634f;  // exp2 units
+  const float grow_thr = kRescaleLog2 / c;
   const uint32_t flip = scale < 0.f ? 0x80008000u : 0u;
-  uint32_t q[NR][4];
+  frag8 qf[D / 32];
+  {
+    const T* qrow = (const T*)p.q + b * p.qs_b + (int64_t)(row / G) * p.qs_s + (kvh * G + row % G) * p.qs_h;
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    u32x4 raw = {0, 0, 0, 0};
-    if (r < p.Sq * G) {
-      const int s = r / G, h = kvh * G + r % G;
-      raw = *(const u32x4*)((const T*)p.q + b * p.qs_b + (int64_t)s * p.qs_s + h * p.qs_h + li * 8);
-    }
+    for (int ks = 0; ks < D / 32; ++ks) {
+      u32x4 raw = {0, 0, 0, 0};
+      if (row_real) raw = *(const u32x4*)(qrow + ks * 32 + grp * 8);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) q[r][w] = raw[w] ^ flip;
-  }
-
-  const char* kb = (const char*)((const T*)p.k[part] + b * p.ks[part][0] + kvh * p.ks[part][2]) + li * 16;
-  const char* vb = (const char*)((const T*)p.v[part] + b * p.vs[part][0] + kvh * p.vs[part][2]) + li * 16;
-  const int64_t krow = p.ks[part][1] * (int64_t)sizeof(T), vrow = p.vs[part][1] * (int64_t)sizeof(T);
-
-  float m[NR], l[NR], o[NR][8];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    m[r] = -__builtin_inff();
-    l[r] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[r][e] = 0.f;
-  }
-
-  for (int bi = 0; bi < nbatch; ++bi) {
-    if (!batch_any[bi]) continue;
-    u32x4 kr[NB], vr[NB];
-    bool kv[NB];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int k = bi * BATCH + u * NGROUPS + grp;
-      bool vis = false;
-      if (k < nkeys) {
-        const int64_t pk = kpos_s[k];
-        vis = pk >= 0 && (!p.causal || pk <= qmax);
-      }
-      kv[u] = vis;
-      kr[u] = {0, 0, 0, 0};
-      vr[u] = {0, 0, 0, 0};
-      if (vis) {
-        kr[u] = *(const u32x4*)(kb + (int64_t)(key0 + k) * krow);
-        vr[u] = *(const u32x4*)(vb + (int64_t)(key0 + k) * vrow);
-      }
-    }
-    float s[NB][NR];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int k = bi * BATCH + u * NGROUPS + grp;
-      const int64_t pk = kv[u] ? kpos_s[k] : -1;
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        float a = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) a = dot2<T>(q[r][w], kr[u][w], a);
-        a = row16_sum(a);
-        const bool ok = kv[u] && (!p.causal || pk <= qp[r]) && qp[r] != INT64_MIN;
-        s[u][r] = ok ? a : -__builtin_inff();
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float mb = s[0][r];
-#pragma unroll
-      for (int u = 1; u < NB; ++u) mb = fmaxf(mb, s[u][r]);
-      const float mn = fmaxf(m[r], mb);
-      if (mn == -__builtin_inff()) continue;  // nothing visible to this row so far
-      const float alpha = __builtin_amdgcn_exp2f((m[r] - mn) * c);
-      m[r] = mn;
-      l[r] *= alpha;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[r][e] *= alpha;
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const float pv = __builtin_amdgcn_exp2f((s[u][r] - mn) * c);
-        l[r] += pv;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          float lo, hi;
-          unpack2<T>(vr[u][w], lo, hi);
-          o[r][2 * w] = __builtin_fmaf(pv, lo, o[r][2 * w]);
-          o[r][2 * w + 1] = __builtin_fmaf(pv, hi, o[r][2 * w + 1]);
-        }
-      }
+      for (int w = 0; w < 4; ++w) raw[w] ^= flip;
+      __builtin_memcpy(&qf[ks], &raw, 16);
     }
   }
 
-  // ---- merge the 16 group partials of the workgroup and write the chunk partial
-  if (li == 0) {
+  // ---- per-lane constant offsets
+  const char* kbase = (const char*)((const T*)p.k[part] + b * p.ks[part][0] + kvh * p.ks[part][2]);
+  const char* vbase = (const char*)((const T*)p.v[part] + b * p.vs[part][0] + kvh * p.vs[part][2]);
+  const uint32_t krow = (uint32_t)(p.ks[part][1] * sizeof(T)), vrow = (uint32_t)(p.vs[part][1] * sizeof(T));
+  uint32_t k_voff[L::LOADS], v_voff[L::LOADS];
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      red_m[grp][r] = m[r];
-      red_l[grp][r] = l[r];
+  for (int i = 0; i < L::LOADS; ++i) {
+    const int r = i * (1024 / L::ROW) + lane / (L::ROW / 16);
+    const int pg = lane % (L::ROW / 16);                   // physical 16-byte group
+    k_voff[i] = r * krow + ((pg ^ (r & 15)) << 4);          // K: 16-byte groups ^ row
+    const int lgv = ((((pg >> 1) ^ (r & 7)) << 1) | (pg & 1));  // V: 32-byte blocks ^ row
+    v_voff[i] = r * vrow + (lgv << 4);
+  }
+  uint32_t k_raddr[D / 32];  // A operand of S: key 'row', features grp*8 + 32*ks
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) k_raddr[ks] = row * L::ROW + (((grp + 4 * ks) ^ (row & 15)) << 4);
+  uint32_t v_raddr[D / 16];  // transposing reads: source lane s of group grp -> key grp*4 + s/4
+  {
+    const int vr = grp * 4 + (row >> 2);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      v_raddr[dt] = L::TILE_BYTES + vr * L::ROW + ((dt ^ (vr & 7)) << 5) + 8 * (row & 3);
+  }
+
+  char* wb = dsmem + wave * L::WAVE_BYTES;
+  auto next_tile = [&](int t) -> int {
+    for (t += NW; t < ntile; t += NW)
+      if (tile_any[t]) return t;
+    return -1;
+  };
+  auto load_tile = [&](int t, int buf) {
+    const int k0 = key0 + t * TK;
+    const uint32_t rows = (uint32_t)min(Sk - k0, TK);  // rows past the end of the keys read 0
+    const i32x4 krs = make_rsrc(kbase + (int64_t)k0 * krow, (rows - 1) * krow + L::ROW);
+    const i32x4 vrs = make_rsrc(vbase + (int64_t)k0 * vrow, (rows - 1) * vrow + L::ROW);
+    char* kb = wb + buf * L::BUF_BYTES;
+#pragma unroll
+    for (int i = 0; i < L::LOADS; ++i) buffer_load_lds16(krs, kb + i * 1024, k_voff[i]);
+#pragma unroll
+    for (int i = 0; i < L::LOADS; ++i) buffer_load_lds16(vrs, kb + L::TILE_BYTES + i * 1024, v_voff[i]);
+  };
+
+  f32x4 o[D / 16];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -__builtin_inff(), m_use = 0.f, l_run = 0.f;
+
+  auto compute = [&](int t, int buf) {
+    const char* kb = wb + buf * L::BUF_BYTES;
+    frag8 kf[D / 32];
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) kf[ks] = *(const frag8*)(kb + k_raddr[ks]);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) s = Mfma16<T>::qk(kf[ks], qf[ks], s);
+    // lane holds keys t*16 + grp*4 + i of query row 'row'
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = t * TK + grp * 4 + i;
+      const int64_t pk = k < nkeys ? kpos_s[k] : -1;
+      const bool vis = row_real && pk >= 0 && (!p.causal || pk <= qpos);
+      if (!vis) s[i] = -__builtin_inff();
+    }
+    float mx = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), __builtin_fmaxf(s[2], s[3]));
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = max_halves(mx);
+    const bool grow = mx > m_run + grow_thr;
+    if (__ballot(grow) != 0) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = grow ? __builtin_amdgcn_exp2f((m_run - m_new) * c) : 1.f;
+      m_run = m_new;
+      m_use = m_run == -__builtin_inff() ? 0.f : m_run * c;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) o[dt] *= alpha;
+    }
+    float pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c, -m_use));
+    l_run += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+    const s16x4 pf = Mfma16<T>::pack(pv[0], pv[1], pv[2], pv[3]);
+    s16x4 vf[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      vf[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(kb + v_raddr[dt]));
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) o[dt] = Mfma16<T>::pv(vf[dt], pf, o[dt]);
+  };
+
+  // ---- per-wave stream over its tiles (wave w: tiles w, w+NW, ...), one tile ahead
+  {
+    int t = next_tile(wave - NW);
+    int buf = 0;
+    if (t >= 0) load_tile(t, 0);
+    while (t >= 0) {
+      const int tn = next_tile(t);
+      if (tn >= 0) {
+        wait_lgkmcnt0();  // the previous tile's LDS reads of buffer buf^1 have completed
+        load_tile(tn, buf ^ 1);
+        wait_vmcnt<2 * L::LOADS>();  // tile t landed; tile tn may still be in flight
+      } else {
+        wait_vmcnt<0>();
+      }
+      compute(t, buf);
+      t = tn;
+      buf ^= 1;
     }
   }
+
+  // ---- merge the waves of the workgroup and write the chunk partial
+  float l_row = l_run + __shfl_xor(l_run, 16, 64);
+  l_row = sum_halves(l_row);
+  if (grp == 0 && row < NR) {
+    red_m[wave][row] = m_run == -__builtin_inff() ? m_run : m_run * fabsf(scale);
+    red_l[wave][row] = l_row;
+  }
+  float* red_o = (float*)wb;  // this wave's own buffer, no longer read by the tile loop
+  if (row < NR) {
 #pragma unroll
-  for (int r = 0; r < NR; ++r)
+    for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red_o[grp][r][li * 8 + e] = o[r][e];
+      for (int i = 0; i < 4; ++i) red_o[row * D + dt * 16 + grp * 4 + i] = o[dt][i];
+  }
   __syncthreads();
   for (int i = tid; i < NR * D; i += DTHREADS) {
     const int r = i / D, d = i % D;
     float M = -__builtin_inff();
 #pragma unroll
-    for (int gi = 0; gi < NGROUPS; ++gi) M = fmaxf(M, red_m[gi][r]);
-    float acc = 0.f, L = 0.f;
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, red_m[w][r]);
+    float acc = 0.f, Lsum = 0.f;
     if (M != -__builtin_inff()) {
 #pragma unroll
-      for (int gi = 0; gi < NGROUPS; ++gi) {
-        const float w = __builtin_amdgcn_exp2f((red_m[gi][r] - M) * c);  // -inf -> 0
-        acc = __builtin_fmaf(red_o[gi][r][d], w, acc);
-        L = __builtin_fmaf(red_l[gi][r], w, L);
+      for (int w = 0; w < NW; ++w) {
+        if (red_m[w][r] == -__builtin_inff()) continue;
+        const float wt = expf(red_m[w][r] - M);
+        acc = __builtin_fmaf(((const float*)(dsmem + w * L::WAVE_BYTES))[r * D + d], wt, acc);
+        Lsum = __builtin_fmaf(red_l[w][r], wt, Lsum);
       }
     }
     part_out[r * (D + 2) + d] = acc;
     if (d == 0) {
-      part_out[r * (D + 2) + D] = M == -__builtin_inff() ? M : M * fabsf(scale);
-      part_out[r * (D + 2) + D + 1] = L;
+      part_out[r * (D + 2) + D] = M;
+      part_out[r * (D + 2) + D + 1] = Lsum;
     }
   }
 }
@@ -278,20 +347,47 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(const DecodeParams p) 
   const int total_chunks = p.chunk_begin[p.nparts];
   const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * total_chunks * NR * (D + 2) + r * (D + 2);
 
+  constexpr int WCH = 4 * D;  // chunk weights staged per round
+  __shared__ float w_s[WCH];
+  __shared__ float l_s[WCH];
+  __shared__ float red[D / 64];
+  const int64_t cstride = (int64_t)NR * (D + 2);
+
   float lse_p[CEA_MAX_PARTS], out_p[CEA_MAX_PARTS];
   for (int part = 0; part < p.nparts; ++part) {
-    float M = -__builtin_inff();
-    for (int ch = p.chunk_begin[part]; ch < p.chunk_begin[part + 1]; ++ch)
-      M = fmaxf(M, base[(int64_t)ch * NR * (D + 2) + D]);
+    const int c0 = p.chunk_begin[part], c1 = p.chunk_begin[part + 1];
+    // reference maximum over the partition's chunks (all threads, then the workgroup)
+    float mx = -__builtin_inff();
+    for (int ch = c0 + d; ch < c1; ch += D) mx = fmaxf(mx, base[ch * cstride + D]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if ((d & 63) == 0) red[d >> 6] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int i = 1; i < D / 64; ++i) M = fmaxf(M, red[i]);
+    __syncthreads();
     float acc = 0.f, L = 0.f;
     if (M != -__builtin_inff()) {
-      for (int ch = p.chunk_begin[part]; ch < p.chunk_begin[part + 1]; ++ch) {
-        const float* pc = base + (int64_t)ch * NR * (D + 2);
-        const float mc = pc[D];
-        if (mc == -__builtin_inff()) continue;
-        const float w = expf(mc - M);
-        acc = __builtin_fmaf(pc[d], w, acc);
-        L = __builtin_fmaf(pc[D + 1], w, L);
+      for (int cb = c0; cb < c1; cb += WCH) {
+        const int n = min(WCH, c1 - cb);
+        for (int j = d; j < n; j += D) {
+          const float mc = base[(cb + j) * cstride + D];
+          const float w = mc == -__builtin_inff() ? 0.f : expf(mc - M);
+          w_s[j] = w;
+          l_s[j] = w == 0.f ? 0.f : base[(cb + j) * cstride + D + 1];
+        }
+        __syncthreads();
+        // independent loads across chunks; chunks without visible keys hold no output
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) {
+          const float w = w_s[j];
+          if (w != 0.f) {
+            acc = __builtin_fmaf(base[(cb + j) * cstride + d], w, acc);
+            L = __builtin_fmaf(l_s[j], w, L);
+          }
+        }
+        __syncthreads();
       }
     }
     const bool empty = !(L > 0.f);
@@ -343,8 +439,17 @@ template <typename T, int D, int NR>
 int launch_nr(const DecodeParams& p, hipStream_t st) {
   const int total = p.chunk_begin[p.nparts];
   if (total > 0) {
-    hipLaunchKernelGGL((decode_split_kernel<T, D, NR>), dim3(total, p.Hkv, p.B), dim3(DTHREADS), 0,
-                       st, p);
+    static bool configured = false;
+    if (!configured) {
+      hipError_t e = hipFuncSetAttribute((const void*)decode_split_kernel<T, D, NR>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         DLayout<D>::LDS_BYTES);
+      CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "decode: cannot reserve %d bytes of LDS: %s",
+                  DLayout<D>::LDS_BYTES, hipGetErrorString(e));
+      configured = true;
+    }
+    hipLaunchKernelGGL((decode_split_kernel<T, D, NR>), dim3(total, p.Hkv, p.B), dim3(DTHREADS),
+                       DLayout<D>::LDS_BYTES, st, p);
     CEA_CHECK_LAUNCH("decode_split");
   }
   const int rows = p.B * p.Sq * p.Hq;
@@ -365,6 +470,8 @@ int launch_d(const DecodeParams& p, int nr, hipStream_t st) {
     case 1: return launch_nr<T, D, 1>(p, st);
     case 2: return launch_nr<T, D, 2>(p, st);
     case 4: return launch_nr<T, D, 4>(p, st);
+    case 8: return launch_nr<T, D, 8>(p, st);
+    case 16: return launch_nr<T, D, 16>(p, st);
   }
   set_error("decode: %d query rows per kv head not supported", nr);
   return CEA_EUNSUPPORTED;
@@ -374,28 +481,28 @@ int launch_d(const DecodeParams& p, int nr, hipStream_t st) {
 
 int decode_rows(int32_t Sq, int32_t G) {
   const int r = Sq * G;
-  return r <= 1 ? 1 : r <= 2 ? 2 : r <= 4 ? 4 : 0;
+  return r <= 1 ? 1 : r <= 2 ? 2 : r <= 4 ? 4 : r <= 8 ? 8 : r <= 16 ? 16 : 0;
 }
 
 bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype,
                       const HeadMap& map) {
   if (!(dtype == CEA_BF16 || dtype == CEA_F16)) return false;
-  if (D != 128) return false;  // a 16-lane group covers one 256-byte row
+  if (D != 128) return false;
   if (map.group <= 0) return false;  // regular GQA grouping only
   return decode_rows(Sq, Hq / Hkv) != 0;
 }
 
 int decode_plan_chunk(int64_t keys_per_head, int32_t B, int32_t Hkv) {
-  // enough work items to fill 256 CUs several times, chunks of 256..2048 keys
+  // enough work items to fill 256 CUs several times, chunks of 256..1024 keys
   const int64_t heads = (int64_t)B * Hkv;
   int ch = 256;
-  while (ch < 2048 && heads * ((keys_per_head + ch - 1) / ch) > 16384) ch *= 2;
+  while (ch < CHMAX && heads * ((keys_per_head + ch - 1) / ch) > 16384) ch *= 2;
   return ch;
 }
 
 int launch_attn_decode(const DecodeParams& p, hipStream_t st) {
   const int nr = decode_rows(p.Sq, p.G);
-  CEA_REQUIRE(p.chunk <= 2048 && p.chunk % BATCH == 0, CEA_EINVAL, "decode: bad chunk %d", p.chunk);
+  CEA_REQUIRE(p.chunk <= CHMAX && p.chunk % TK == 0, CEA_EINVAL, "decode: bad chunk %d", p.chunk);
   if (p.D == 128 && p.in_dtype == CEA_BF16) return launch_d<bf16, 128>(p, nr, st);
   if (p.D == 128 && p.in_dtype == CEA_F16) return launch_d<f16, 128>(p, nr, st);
   set_error("decode: unsupported dtype %s / head size %d", dtype_name(p.in_dtype), p.D);

@@ -29,6 +29,7 @@
 //     query-position range, so causal, zigzag and padding masks cost nothing on tiles that
 //     are entirely visible or entirely hidden.
 #include "cea_kernels.hpp"
+#include "cea_lds_dma.hpp"
 
 namespace cea {
 namespace {
@@ -37,7 +38,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
 template <typename T> struct Mfma;
@@ -61,7 +61,6 @@ constexpr int BN = kTileKeys;     // keys per tile
 constexpr int NSTAGE = 4;         // LDS ring depth (NSTAGE - 1 tiles in flight)
 constexpr int LIST_CAP = 2048;    // tiles listed per pass over the key block
 constexpr float kRescaleLog2 = 8.0f;    // lazy-rescale threshold, log2 units
-constexpr int kRsrcFlags = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 
 template <int D> struct Layout {
   static constexpr int KROW = D * 2;                 // bytes per K / V row
@@ -87,43 +86,6 @@ template <int D> __device__ __forceinline__ int v_swz(int key) {
   if constexpr (D == 128) return key & 3;
   else return (key >> 1) & 1;
 }
-
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer resource: base, stride 0, num_records = bytes (reads at or past it return 0).
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  i32x4 r;
-  r[0] = (int32_t)(uint32_t)a;
-  r[1] = (int32_t)((uint32_t)(a >> 32) & 0xffffu);
-  r[2] = (int32_t)bytes;
-  r[3] = kRsrcFlags;
-  return r;
-}
-
-// LDS byte address of a wave-uniform pointer, in an SGPR (M0 takes scalar operands only)
-__device__ __forceinline__ uint32_t lds_addr(const char* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_ptr)p);
-}
-
-// Buffer loads straight into LDS (M0 = LDS base, lane l writes base + l*size).  Issued as
-// inline assembly: the kernel waits for them explicitly with vmcnt, and the compiler, which
-// cannot tell which LDS bytes they write, would otherwise drain every load in flight before
-// each LDS read.  A load the compiler does not see can only make its own waits stricter.
-__device__ __forceinline__ void buffer_load_lds16(i32x4 rs, const char* lds_base, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               ::"s"(lds_addr(lds_base)), "v"(voffset), "s"(rs) : "memory", "m0");
-}
-// 4 bytes per lane (exact per-dword range check: a pair of positions that straddles the end
-// of the key block cannot lose its valid half)
-__device__ __forceinline__ void buffer_load_lds4(i32x4 rs, const char* lds_base, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-               ::"s"(lds_addr(lds_base)), "v"(voffset), "s"(rs) : "memory", "m0");
-}
-
-// Workgroup barrier that keeps the compiler from moving memory operations across it without
-// forcing outstanding buffer loads to complete (the pipeline waits for them explicitly).
-__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
 
 template <typename F>
 __device__ __forceinline__ F read_tr_frag(const char* a0, const char* a1) {

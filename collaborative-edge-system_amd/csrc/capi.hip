@@ -220,6 +220,7 @@ static bool use_decode(const AttnParams& p) {
   const int64_t s8[] = {p.qs_b, p.qs_s, p.qs_h, p.ks_b, p.ks_s, p.ks_h, p.vs_b, p.vs_s, p.vs_h};
   for (int64_t s : s8)
     if (s % 8) return false;
+  if (p.ks_s > (1 << 24) || p.vs_s > (1 << 24)) return false;  // 16-row tile spans stay 32-bit
   return ((uintptr_t)p.q & 15) == 0 && ((uintptr_t)p.k & 15) == 0 && ((uintptr_t)p.v & 15) == 0;
 }
 
