@@ -4,7 +4,7 @@
 // is a few tokens, and the per-device compute of distributed_kv_attention
 // (collab_infer/parallel/sequence_parallel.py:250-280): every KV partition's partial
 // (out, lse) and their exact merge (merge_attention_list, attention.py:253-264), all on one
-// device and in two launches.
+// device and in three launches.
 //
 // HBM-bound design:
 //   * work item = (batch, kv head, key chunk of one partition); the NR = Sq*G query rows that
@@ -13,16 +13,19 @@
 //     off the vector ALU: S = K.Q^T with v_mfma_f32_16x16x32 (a lane holds 4 keys of one
 //     query row) and O^T += V^T.P^T with v_mfma_f32_16x16x16 (P is the score tile as is);
 //   * every wave streams its own 16-key tiles of K and V straight into a private pair of LDS
-//     buffers (buffer_load ... lds, one tile ahead, explicit vmcnt waits, no barriers); V is
+//     buffers (non-temporal buffer_load ... lds, explicit vmcnt waits, no barriers); a buffer
+//     is refilled as soon as its fragments are in registers, so two tiles stay in flight; V is
 //     read back transposed with ds_read_b64_tr_b16; both tiles are XOR-swizzled so the
 //     fragment and transpose reads are free of LDS bank conflicts;
-//   * key positions of the chunk are staged in LDS; 16-key tiles that no query row can see
-//     are never loaded, and chunks past every valid key return after the position scan;
+//   * a prepass reads the key positions once per batch row (not once per kv head) and turns
+//     them into a 16-bit visibility word per key (bit s: query s sees it) and a mask of the
+//     16-key tiles of each chunk that hold a visible key; the split kernel loads each tile's
+//     words with its K and V, never loads an invisible tile, and leaves a chunk with an empty
+//     mask after one scalar load;
 //   * the waves of a workgroup merge their online-softmax partials in LDS and write one
 //     (o unnormalised, m, l) partial per chunk; the reduction kernel then merges the chunks
-//     of each partition exactly (optionally emitting each partition's (out, lse)), merges the
-//     partitions with the reference's logsumexp, and writes out (f32 or the query dtype) and
-//     lse.
+//     (optionally emitting each partition's (out, lse)), computes lse with the reference's
+//     logsumexp over partitions, and writes out (f32 or the query dtype) and lse.
 #include "cea_kernels.hpp"
 #include "cea_lds_dma.hpp"
 
@@ -32,8 +35,14 @@ namespace {
 constexpr int DTHREADS = 256;
 constexpr int NW = DTHREADS / 64;     // waves per workgroup
 constexpr int TK = 16;                // keys per tile
-constexpr int CHMAX = 1024;           // keys per chunk at most
-constexpr int NTILE_MAX = CHMAX / TK;
+#ifndef CEA_DECODE_CHMAX
+#define CEA_DECODE_CHMAX 1024
+#endif
+#ifndef CEA_DECODE_ITEMS
+#define CEA_DECODE_ITEMS 8192
+#endif
+constexpr int CHMAX = CEA_DECODE_CHMAX;  // keys per chunk at most
+static_assert(CHMAX % DTHREADS == 0 && CHMAX <= 4 * DTHREADS, "one 64-bit tile mask per chunk");
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold, log2 units
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -83,7 +92,8 @@ template <> struct Mfma16<f16> {
 template <int D> struct DLayout {
   static constexpr int ROW = D * 2;                 // bytes per key row
   static constexpr int TILE_BYTES = TK * ROW;       // one K or V tile
-  static constexpr int BUF_BYTES = 2 * TILE_BYTES;  // K + V
+  static constexpr int VIS_OFF = 2 * TILE_BYTES;    // 16 visibility words after K and V
+  static constexpr int BUF_BYTES = VIS_OFF + 64;
   static constexpr int WAVE_BYTES = 2 * BUF_BYTES;  // double-buffered per wave
   static constexpr int LDS_BYTES = NW * WAVE_BYTES;
   static constexpr int LOADS = TILE_BYTES / 1024;   // direct loads per tensor per tile
@@ -106,6 +116,57 @@ __device__ __forceinline__ int part_of(const DecodeParams& p, int chunk) {
   return part;
 }
 
+// Visibility prepass, one workgroup per (chunk, batch): for every key of the chunk a word whose
+// bit s says whether query s of the batch sees it (k_pos >= 0 and, when causal,
+// k_pos <= q_pos[s]), and for the chunk a mask of the 16-key tiles holding a visible key.
+// The split kernel then never reads positions, and skips invisible tiles without loading them.
+__global__ __launch_bounds__(DTHREADS) void decode_vis_kernel(const DecodeParams p) {
+  const int chunk = blockIdx.x, b = blockIdx.y;
+  const int part = part_of(p, chunk);
+  const int key0 = (chunk - p.chunk_begin[part]) * p.chunk;
+  const int nkeys = min(p.chunk, p.Sk[part] - key0);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int total_chunks = p.chunk_begin[p.nparts];
+  __shared__ int64_t qp[16];
+  __shared__ uint32_t wmask[NW];
+  if (tid < p.Sq) qp[tid] = p.q_pos[b * p.qps_b + (int64_t)tid * p.qps_s];
+  __syncthreads();
+  const int64_t* kp = p.k_pos[part] + b * p.kps[part][0];
+  const int64_t kps = p.kps[part][1];
+  uint32_t words[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int k = tid * 4 + u;
+    uint32_t w = 0;
+    if (k < nkeys) {
+      const int64_t pk = kp[(int64_t)(key0 + k) * kps];
+      if (pk >= 0)
+        for (int q = 0; q < p.Sq; ++q)
+          if (!p.causal || pk <= qp[q]) w |= 1u << q;
+    }
+    words[u] = w;
+  }
+  if (tid * 4 < p.chunk) {
+    uint2 packed = {words[0] | (words[1] << 16), words[2] | (words[3] << 16)};
+    *(uint2*)(p.vis + ((int64_t)b * total_chunks + chunk) * p.chunk + tid * 4) = packed;
+  }
+  // lanes 4j..4j+3 of wave w hold tile w*16 + j
+  const uint64_t bal = __ballot((words[0] | words[1] | words[2] | words[3]) != 0);
+  if (lane == 0) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) m |= (((bal >> (4 * j)) & 0xfu) != 0 ? 1u : 0u) << j;
+    wmask[wave] = m;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t m = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) m |= (uint64_t)wmask[w] << (16 * w);
+    p.tile_mask[(int64_t)b * total_chunks + chunk] = m;
+  }
+}
+
 // Partial layout: [B][Hkv][total_chunks][NR][D + 2] floats: o (relative to m), m, l, where
 // m is in natural-log units (max of scale*q.k) and l = sum exp(scale*q.k - m).
 template <typename T, int D, int NR>
@@ -113,60 +174,29 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   typedef DLayout<D> L;
   typedef typename Mfma16<T>::frag8 frag8;
   extern __shared__ __attribute__((aligned(16))) char dsmem[];
-  __shared__ int64_t kpos_s[CHMAX];
-  __shared__ uint32_t tile_any[NTILE_MAX];
   __shared__ float red_m[NW][NR];
   __shared__ float red_l[NW][NR];
 
   const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int part = part_of(p, chunk);
-  const int lchunk = chunk - p.chunk_begin[part];
-  const int Sk = p.Sk[part];
-  const int key0 = lchunk * p.chunk;
-  const int nkeys = min(p.chunk, Sk - key0);
-  const int ntile = (nkeys + TK - 1) / TK;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int row = lane & 15;   // query row (MFMA column) of this lane
-  const int grp = lane >> 4;   // 4-key group of the 16-key tile
-  const int G = p.G;
-  const int nreal = p.Sq * G;
   const int total_chunks = p.chunk_begin[p.nparts];
   float* part_out = p.partial + (((int64_t)b * p.Hkv + kvh) * total_chunks + chunk) * NR * (D + 2);
-
-  // ---- query rows of this kv head: row r = (s, gi) -> head kvh*G + gi, position q_pos[b, s]
-  const bool row_real = row < nreal;
-  const int64_t qpos = row_real ? p.q_pos[b * p.qps_b + (int64_t)(row / G) * p.qps_s] : INT64_MIN;
-  int64_t qmax = INT64_MIN;
-  for (int r = 0; r < nreal; ++r) {
-    const int64_t v = p.q_pos[b * p.qps_b + (int64_t)(r / G) * p.qps_s];
-    qmax = v > qmax ? v : qmax;
-  }
-
-  // ---- positions of the chunk into LDS; which 16-key tiles have a visible key
-  const int64_t* kp = p.k_pos[part] + b * p.kps[part][0];
-  const int64_t kps = p.kps[part][1];
-  for (int i = tid; i < nkeys; i += DTHREADS) kpos_s[i] = kp[(int64_t)(key0 + i) * kps];
-  __syncthreads();
-  for (int t0 = wave * 4; t0 < ntile; t0 += NW * 4) {
-    const int k = t0 * TK + lane;
-    bool vis = false;
-    if (k < nkeys) {
-      const int64_t pk = kpos_s[k];
-      vis = pk >= 0 && (!p.causal || pk <= qmax);
-    }
-    const uint64_t bal = __ballot(vis);
-    if (lane < 4 && t0 + lane < ntile) tile_any[t0 + lane] = (uint32_t)((bal >> (16 * lane)) & 0xffffu);
-  }
-  __syncthreads();
-  bool any = false;
-  for (int t = 0; t < ntile; ++t) any |= tile_any[t] != 0;
-  if (!any) {
+  const uint64_t mask = p.tile_mask[(int64_t)b * total_chunks + chunk];
+  if (mask == 0) {  // no key of the chunk is visible to any query row
     if (tid < NR) {
       part_out[tid * (D + 2) + D] = -__builtin_inff();
       part_out[tid * (D + 2) + D + 1] = 0.f;
     }
     return;
   }
+  const int part = part_of(p, chunk);
+  const int Sk = p.Sk[part];
+  const int key0 = (chunk - p.chunk_begin[part]) * p.chunk;
+  const int row = lane & 15;   // query row (MFMA column) of this lane
+  const int grp = lane >> 4;   // 4-key group of the 16-key tile
+  const int G = p.G;
+  const bool row_real = row < p.Sq * G;
+  const int qbit = row / G;    // query index s of this row
 
   // ---- this lane's Q fragments (B operand of S = K.Q^T), sign folded for a negative scale
   const float scale = (float)p.scale;
@@ -175,20 +205,25 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   const uint32_t flip = scale < 0.f ? 0x80008000u : 0u;
   frag8 qf[D / 32];
   {
-    const T* qrow = (const T*)p.q + b * p.qs_b + (int64_t)(row / G) * p.qs_s + (kvh * G + row % G) * p.qs_h;
+    // padding rows (row >= Sq*G) read query row 0 and zero it
+    const int qr = row_real ? row : 0;
+    const T* qrow = (const T*)p.q + b * p.qs_b + (int64_t)(qr / G) * p.qs_s + (kvh * G + qr % G) * p.qs_h;
+    u32x4 raw[D / 32];
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) raw[ks] = *(const u32x4*)(qrow + ks * 32 + grp * 8);
+    const uint32_t keep = row_real ? 0xffffffffu : 0u;
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
-      u32x4 raw = {0, 0, 0, 0};
-      if (row_real) raw = *(const u32x4*)(qrow + ks * 32 + grp * 8);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) raw[w] ^= flip;
-      __builtin_memcpy(&qf[ks], &raw, 16);
+      for (int w = 0; w < 4; ++w) raw[ks][w] = (raw[ks][w] ^ flip) & keep;
+      __builtin_memcpy(&qf[ks], &raw[ks], 16);
     }
   }
 
   // ---- per-lane constant offsets
   const char* kbase = (const char*)((const T*)p.k[part] + b * p.ks[part][0] + kvh * p.ks[part][2]);
   const char* vbase = (const char*)((const T*)p.v[part] + b * p.vs[part][0] + kvh * p.vs[part][2]);
+  const char* visbase = (const char*)(p.vis + ((int64_t)b * total_chunks + chunk) * p.chunk);
   const uint32_t krow = (uint32_t)(p.ks[part][1] * sizeof(T)), vrow = (uint32_t)(p.vs[part][1] * sizeof(T));
   uint32_t k_voff[L::LOADS], v_voff[L::LOADS];
 #pragma unroll
@@ -211,10 +246,13 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   }
 
   char* wb = dsmem + wave * L::WAVE_BYTES;
-  auto next_tile = [&](int t) -> int {
-    for (t += NW; t < ntile; t += NW)
-      if (tile_any[t]) return t;
-    return -1;
+  // this wave's tiles: wave, wave + NW, ... that hold a visible key
+  uint64_t todo = mask & (0x1111111111111111ull << wave);
+  auto pop_tile = [&]() -> int {
+    if (todo == 0) return -1;
+    const int t = (int)__builtin_ctzll(todo);
+    todo &= todo - 1;
+    return t;
   };
   auto load_tile = [&](int t, int buf) {
     const int k0 = key0 + t * TK;
@@ -223,30 +261,45 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
     const i32x4 vrs = make_rsrc(vbase + (int64_t)k0 * vrow, (rows - 1) * vrow + L::ROW);
     char* kb = wb + buf * L::BUF_BYTES;
 #pragma unroll
-    for (int i = 0; i < L::LOADS; ++i) buffer_load_lds16(krs, kb + i * 1024, k_voff[i]);
+    for (int i = 0; i < L::LOADS; ++i) buffer_load_lds16_nt(krs, kb + i * 1024, k_voff[i]);
 #pragma unroll
-    for (int i = 0; i < L::LOADS; ++i) buffer_load_lds16(vrs, kb + L::TILE_BYTES + i * 1024, v_voff[i]);
+    for (int i = 0; i < L::LOADS; ++i) buffer_load_lds16_nt(vrs, kb + L::TILE_BYTES + i * 1024, v_voff[i]);
+    if (lane < TK * 2 / 4) {  // 16 visibility words, 4 bytes per lane
+      const i32x4 wrs = make_rsrc(visbase + t * TK * 2, TK * 2);
+      buffer_load_lds4(wrs, kb + L::VIS_OFF, lane * 4);
+    }
   };
+  constexpr int LOADS_PER_TILE = 2 * L::LOADS + 1;
 
   f32x4 o[D / 16];
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -__builtin_inff(), m_use = 0.f, l_run = 0.f;
 
-  auto compute = [&](int t, int buf) {
+  // Fragments of one tile, read from LDS before the math so the buffer can be refilled.
+  struct Frags {
+    frag8 k[D / 32];
+    s16x4 v[D / 16];
+    uint2 vis;
+  };
+  auto read_frags = [&](int buf, Frags& f) {
     const char* kb = wb + buf * L::BUF_BYTES;
-    frag8 kf[D / 32];
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) kf[ks] = *(const frag8*)(kb + k_raddr[ks]);
+    for (int ks = 0; ks < D / 32; ++ks) f.k[ks] = *(const frag8*)(kb + k_raddr[ks]);
+    f.vis = *(const uint2*)(kb + L::VIS_OFF + grp * 8);  // keys grp*4 .. grp*4+3
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      f.v[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(kb + v_raddr[dt]));
+  };
+  auto compute = [&](const Frags& f) {
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) s = Mfma16<T>::qk(kf[ks], qf[ks], s);
-    // lane holds keys t*16 + grp*4 + i of query row 'row'
+    for (int ks = 0; ks < D / 32; ++ks) s = Mfma16<T>::qk(f.k[ks], qf[ks], s);
+    // lane holds keys grp*4 + i of the tile for query row 'row'
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int k = t * TK + grp * 4 + i;
-      const int64_t pk = k < nkeys ? kpos_s[k] : -1;
-      const bool vis = row_real && pk >= 0 && (!p.causal || pk <= qpos);
+      const uint32_t word = ((i < 2 ? f.vis.x : f.vis.y) >> (16 * (i & 1))) & 0xffffu;
+      const bool vis = row_real && ((word >> qbit) & 1u);
       if (!vis) s[i] = -__builtin_inff();
     }
     float mx = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), __builtin_fmaxf(s[2], s[3]));
@@ -267,30 +320,37 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
     for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c, -m_use));
     l_run += (pv[0] + pv[1]) + (pv[2] + pv[3]);
     const s16x4 pf = Mfma16<T>::pack(pv[0], pv[1], pv[2], pv[3]);
-    s16x4 vf[D / 16];
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt)
-      vf[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(kb + v_raddr[dt]));
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) o[dt] = Mfma16<T>::pv(vf[dt], pf, o[dt]);
+    for (int dt = 0; dt < D / 16; ++dt) o[dt] = Mfma16<T>::pv(f.v[dt], pf, o[dt]);
   };
 
-  // ---- per-wave stream over its tiles (wave w: tiles w, w+NW, ...), one tile ahead
+  // ---- per-wave stream over its tiles: two buffers, refilled as soon as their fragments are
+  // in registers, so two tiles are in flight during the math of a third
   {
-    int t = next_tile(wave - NW);
+    // Q in registers first: the compiler's wait for it at its first use would otherwise also
+    // drain the tile loads issued by then
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) asm volatile("" ::"v"(qf[ks]));
+    int t = pop_tile();
+    int t1 = pop_tile();
     int buf = 0;
     if (t >= 0) load_tile(t, 0);
+    if (t1 >= 0) load_tile(t1, 1);
     while (t >= 0) {
-      const int tn = next_tile(t);
-      if (tn >= 0) {
-        wait_lgkmcnt0();  // the previous tile's LDS reads of buffer buf^1 have completed
-        load_tile(tn, buf ^ 1);
-        wait_vmcnt<2 * L::LOADS>();  // tile t landed; tile tn may still be in flight
-      } else {
+      if (t1 >= 0)
+        wait_vmcnt<LOADS_PER_TILE>();  // tile t landed; tile t1 may still be in flight
+      else
         wait_vmcnt<0>();
+      Frags f;
+      read_frags(buf, f);
+      const int t2 = pop_tile();
+      if (t2 >= 0) {
+        wait_lgkmcnt0();  // fragments in registers before the buffer is refilled
+        load_tile(t2, buf);
       }
-      compute(t, buf);
-      t = tn;
+      compute(f);
+      t = t1;
+      t1 = t2;
       buf ^= 1;
     }
   }
@@ -333,80 +393,83 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   }
 }
 
-// One workgroup of D threads per (b, s, h) output row: merge the chunks of each partition,
-// then the partitions.
+// Reduction of the chunk partials, one workgroup of RTHREADS per (b, s, h) output row.
+//   1. the (m, l) of every chunk into LDS;
+//   2. per partition: M_p = max m, L_p = sum l * exp(m - M_p), lse_p = M_p + log L_p; then
+//      lse = logsumexp over partitions (the reference merge's formula) and per-chunk weights
+//      W = exp(m - lse), which fold a chunk's partition normalisation and its merge weight;
+//   3. out = sum over chunks of o * W, the waves taking interleaved chunks (all loads of a
+//      row independent), combined in a fixed order.  Partition outputs, when requested, are
+//      the same sums restricted to a partition, times exp(lse - lse_p).
+constexpr int RTHREADS = 256;
+constexpr int RWAVES = RTHREADS / 64;
+constexpr int RCH = kDecodeMaxChunks;  // chunks staged per row
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < RWAVES; ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < RWAVES; ++i) r += red[i];
+  return r;
+}
+
 template <typename O, int D, int NR>
-__global__ __launch_bounds__(D) void decode_reduce_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodeParams p) {
+  static_assert(D == 128, "two output features per lane");
   const int row = blockIdx.x;  // (b, s, h)
   const int h = row % p.Hq;
   const int s = (row / p.Hq) % p.Sq;
   const int b = row / (p.Hq * p.Sq);
-  const int d = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kvh = p.map.kv_of(h);
   const int r = s * p.G + (h - kvh * p.G);
-  const int total_chunks = p.chunk_begin[p.nparts];
-  const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * total_chunks * NR * (D + 2) + r * (D + 2);
-
-  constexpr int WCH = 4 * D;  // chunk weights staged per round
-  __shared__ float w_s[WCH];
-  __shared__ float l_s[WCH];
-  __shared__ float red[D / 64];
+  const int total = p.chunk_begin[p.nparts];
   const int64_t cstride = (int64_t)NR * (D + 2);
+  const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * total * cstride + r * (D + 2);
 
-  float lse_p[CEA_MAX_PARTS], out_p[CEA_MAX_PARTS];
+  __shared__ float m_s[RCH];
+  __shared__ float w_s[RCH];
+  __shared__ float red[RWAVES];
+  __shared__ float2 acc_s[RWAVES][D / 2];
+
+  for (int j = tid; j < total; j += RTHREADS) {
+    m_s[j] = base[j * cstride + D];
+    w_s[j] = base[j * cstride + D + 1];  // l, replaced by the weight below
+  }
+  __syncthreads();
+  float lse_p[CEA_MAX_PARTS];
   for (int part = 0; part < p.nparts; ++part) {
     const int c0 = p.chunk_begin[part], c1 = p.chunk_begin[part + 1];
-    // reference maximum over the partition's chunks (all threads, then the workgroup)
     float mx = -__builtin_inff();
-    for (int ch = c0 + d; ch < c1; ch += D) mx = fmaxf(mx, base[ch * cstride + D]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if ((d & 63) == 0) red[d >> 6] = mx;
-    __syncthreads();
-    float M = red[0];
-#pragma unroll
-    for (int i = 1; i < D / 64; ++i) M = fmaxf(M, red[i]);
-    __syncthreads();
-    float acc = 0.f, L = 0.f;
-    if (M != -__builtin_inff()) {
-      for (int cb = c0; cb < c1; cb += WCH) {
-        const int n = min(WCH, c1 - cb);
-        for (int j = d; j < n; j += D) {
-          const float mc = base[(cb + j) * cstride + D];
-          const float w = mc == -__builtin_inff() ? 0.f : expf(mc - M);
-          w_s[j] = w;
-          l_s[j] = w == 0.f ? 0.f : base[(cb + j) * cstride + D + 1];
-        }
-        __syncthreads();
-        // independent loads across chunks; chunks without visible keys hold no output
-#pragma unroll 8
-        for (int j = 0; j < n; ++j) {
-          const float w = w_s[j];
-          if (w != 0.f) {
-            acc = __builtin_fmaf(base[(cb + j) * cstride + d], w, acc);
-            L = __builtin_fmaf(l_s[j], w, L);
-          }
-        }
-        __syncthreads();
-      }
-    }
-    const bool empty = !(L > 0.f);
-    lse_p[part] = empty ? -__builtin_inff() : M + logf(L);
-    out_p[part] = empty ? 0.f : acc / L;
-    if (p.part_out[part]) {
-      float* po = (float*)p.part_out[part] + b * p.pos_[part][0] + s * p.pos_[part][1] + h * p.pos_[part][2];
-      po[d] = out_p[part];
-      if (d == 0) {
-        float* pl = (float*)p.part_lse[part] + b * p.pls_[part][0] + h * p.pls_[part][1] + s * p.pls_[part][2];
-        *pl = lse_p[part];
-      }
-    }
+    for (int j = c0 + tid; j < c1; j += RTHREADS) mx = fmaxf(mx, m_s[j]);
+    const float M = block_max(mx, red);
+    float l = 0.f;
+    if (M != -__builtin_inff())
+      for (int j = c0 + tid; j < c1; j += RTHREADS)
+        if (m_s[j] != -__builtin_inff()) l = __builtin_fmaf(w_s[j], expf(m_s[j] - M), l);
+    const float L = block_sum(l, red);
+    lse_p[part] = L > 0.f ? M + logf(L) : -__builtin_inff();
   }
-  // merge of the partitions: logsumexp and weighted sum in partition order
-  float lse, res;
+  float lse;
   if (p.nparts == 1) {
     lse = lse_p[0];
-    res = out_p[0];
   } else {
     float mx = -__builtin_inff();
     for (int part = 0; part < p.nparts; ++part) mx = fmaxf(mx, lse_p[part]);
@@ -414,24 +477,75 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(const DecodeParams p) 
     float sum = 0.f;
     for (int part = 0; part < p.nparts; ++part) sum = add_rn(sum, expf(lse_p[part] - shift));
     lse = logf(sum) + shift;
-    const float safe = is_finite(lse) ? lse : 0.f;
-    res = 0.f;
-    for (int part = 0; part < p.nparts; ++part)
-      res = add_rn(res, mul_rn(out_p[part], expf(lse_p[part] - safe)));
   }
+  const bool empty = lse == -__builtin_inff();
+  __syncthreads();  // every thread has read the l values
+  for (int j = tid; j < total; j += RTHREADS)
+    w_s[j] = (empty || m_s[j] == -__builtin_inff()) ? 0.f : expf(m_s[j] - lse);
+  __syncthreads();
+
+  // weighted sum of the chunk outputs over [c0, c1): wave w takes chunks c0 + w, c0 + w + 4, ...
+  auto chunk_sum = [&](int c0, int c1) -> float2 {
+    float2 a = {0.f, 0.f};
+#pragma unroll 8
+    for (int j = c0 + wave; j < c1; j += RWAVES) {
+      // chunks without a visible key have weight 0 and unwritten outputs: select, not multiply
+      const float w = w_s[j];
+      const float2 o = *(const float2*)(base + j * cstride + 2 * lane);
+      a.x = w != 0.f ? __builtin_fmaf(o.x, w, a.x) : a.x;
+      a.y = w != 0.f ? __builtin_fmaf(o.y, w, a.y) : a.y;
+    }
+    acc_s[wave][lane] = a;
+    __syncthreads();
+    float2 t = acc_s[0][lane];
+#pragma unroll
+    for (int i = 1; i < RWAVES; ++i) {
+      t.x += acc_s[i][lane].x;
+      t.y += acc_s[i][lane].y;
+    }
+    __syncthreads();
+    return t;
+  };
+
+  float2 res;
+  if (p.part_out[0]) {
+    res = {0.f, 0.f};
+    for (int part = 0; part < p.nparts; ++part) {
+      const float2 t = chunk_sum(p.chunk_begin[part], p.chunk_begin[part + 1]);
+      res.x += t.x;
+      res.y += t.y;
+      if (wave == 0) {
+        const bool pe = lse_p[part] == -__builtin_inff();
+        const float f = pe ? 0.f : expf(lse - lse_p[part]);
+        float* po = (float*)p.part_out[part] + b * p.pos_[part][0] + s * p.pos_[part][1] + h * p.pos_[part][2];
+        po[2 * lane] = t.x * f;
+        po[2 * lane + 1] = t.y * f;
+        if (lane == 0) {
+          float* pl = (float*)p.part_lse[part] + b * p.pls_[part][0] + h * p.pls_[part][1] + s * p.pls_[part][2];
+          *pl = lse_p[part];
+        }
+      }
+    }
+  } else {
+    res = chunk_sum(0, total);
+  }
+  if (wave != 0) return;
   float* lptr = p.lse ? (float*)p.lse + b * p.ls_b + h * p.ls_h + s * p.ls_s : nullptr;
-  O* optr = (O*)p.out + b * p.os_b + s * p.os_s + h * p.os_h;
+  O* optr = (O*)p.out + b * p.os_b + s * p.os_s + h * p.os_h + 2 * lane;
   if (p.accumulate) {  // merge_attention(running, new)
     const float lse_old = *lptr;
     const float lm = logaddexp<float>(lse_old, lse);
     const float safe = is_finite(lm) ? lm : 0.f;
-    const float v = add_rn(mul_rn((float)optr[d], expf(lse_old - safe)), mul_rn(res, expf(lse - safe)));
-    optr[d] = (O)v;
-    __syncthreads();  // every thread has read lse_old
-    if (d == 0) *lptr = lm;
+    const float fo = expf(lse_old - safe), fn = expf(lse - safe);
+    const float v0 = add_rn(mul_rn((float)optr[0], fo), mul_rn(res.x, fn));
+    const float v1 = add_rn(mul_rn((float)optr[1], fo), mul_rn(res.y, fn));
+    optr[0] = (O)v0;
+    optr[1] = (O)v1;
+    if (lane == 0) *lptr = lm;  // the wave's loads of lse_old precede this store
   } else {
-    optr[d] = (O)res;
-    if (lptr && d == 0) *lptr = lse;
+    optr[0] = (O)res.x;
+    optr[1] = (O)res.y;
+    if (lptr && lane == 0) *lptr = lse;
   }
 }
 
@@ -439,6 +553,8 @@ template <typename T, int D, int NR>
 int launch_nr(const DecodeParams& p, hipStream_t st) {
   const int total = p.chunk_begin[p.nparts];
   if (total > 0) {
+    hipLaunchKernelGGL(decode_vis_kernel, dim3(total, p.B), dim3(DTHREADS), 0, st, p);
+    CEA_CHECK_LAUNCH("decode_vis");
     static bool configured = false;
     if (!configured) {
       hipError_t e = hipFuncSetAttribute((const void*)decode_split_kernel<T, D, NR>,
@@ -455,11 +571,11 @@ int launch_nr(const DecodeParams& p, hipStream_t st) {
   const int rows = p.B * p.Sq * p.Hq;
   if (rows == 0) return CEA_OK;
   if (p.out_dtype == CEA_F32)
-    hipLaunchKernelGGL((decode_reduce_kernel<float, D, NR>), dim3(rows), dim3(D), 0, st, p);
+    hipLaunchKernelGGL((decode_reduce_kernel<float, D, NR>), dim3(rows), dim3(RTHREADS), 0, st, p);
   else if (p.out_dtype == CEA_BF16)
-    hipLaunchKernelGGL((decode_reduce_kernel<bf16, D, NR>), dim3(rows), dim3(D), 0, st, p);
+    hipLaunchKernelGGL((decode_reduce_kernel<bf16, D, NR>), dim3(rows), dim3(RTHREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((decode_reduce_kernel<f16, D, NR>), dim3(rows), dim3(D), 0, st, p);
+    hipLaunchKernelGGL((decode_reduce_kernel<f16, D, NR>), dim3(rows), dim3(RTHREADS), 0, st, p);
   CEA_CHECK_LAUNCH("decode_reduce");
   return CEA_OK;
 }
@@ -496,13 +612,15 @@ int decode_plan_chunk(int64_t keys_per_head, int32_t B, int32_t Hkv) {
   // enough work items to fill 256 CUs several times, chunks of 256..1024 keys
   const int64_t heads = (int64_t)B * Hkv;
   int ch = 256;
-  while (ch < CHMAX && heads * ((keys_per_head + ch - 1) / ch) > 16384) ch *= 2;
+  while (ch < CHMAX && heads * ((keys_per_head + ch - 1) / ch) > CEA_DECODE_ITEMS) ch *= 2;
   return ch;
 }
 
 int launch_attn_decode(const DecodeParams& p, hipStream_t st) {
   const int nr = decode_rows(p.Sq, p.G);
   CEA_REQUIRE(p.chunk <= CHMAX && p.chunk % TK == 0, CEA_EINVAL, "decode: bad chunk %d", p.chunk);
+  CEA_REQUIRE(p.chunk_begin[p.nparts] <= kDecodeMaxChunks, CEA_EUNSUPPORTED,
+              "decode: %d chunks exceed %d", p.chunk_begin[p.nparts], kDecodeMaxChunks);
   if (p.D == 128 && p.in_dtype == CEA_BF16) return launch_d<bf16, 128>(p, nr, st);
   if (p.D == 128 && p.in_dtype == CEA_F16) return launch_d<f16, 128>(p, nr, st);
   set_error("decode: unsupported dtype %s / head size %d", dtype_name(p.in_dtype), p.D);

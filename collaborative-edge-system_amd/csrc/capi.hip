@@ -146,7 +146,8 @@ struct DecodePlan {
   int chunk;
   int total_chunks;
   int nr;
-  size_t partial_bytes;
+  size_t partial_bytes;  // partials + visibility words + tile masks
+  size_t vis_offset, mask_offset;
 };
 
 static DecodePlan plan_decode(const int64_t* Sk, int n, int64_t B, int64_t Sq, int64_t Hq,
@@ -158,8 +159,10 @@ static DecodePlan plan_decode(const int64_t* Sk, int n, int64_t B, int64_t Sq, i
   pl.total_chunks = 0;
   for (int i = 0; i < n; ++i) pl.total_chunks += (int)((Sk[i] + pl.chunk - 1) / pl.chunk);
   pl.nr = decode_rows((int32_t)Sq, (int32_t)(Hq / (Hkv > 0 ? Hkv : 1)));
-  pl.partial_bytes = align_up((size_t)(B * Hkv) * pl.total_chunks * (pl.nr > 0 ? pl.nr : 1) *
-                                  (D + 2) * sizeof(float), 256);
+  pl.vis_offset = align_up((size_t)(B * Hkv) * pl.total_chunks * (pl.nr > 0 ? pl.nr : 1) *
+                               (D + 2) * sizeof(float), 256);
+  pl.mask_offset = pl.vis_offset + align_up((size_t)B * pl.total_chunks * pl.chunk * sizeof(uint16_t), 256);
+  pl.partial_bytes = pl.mask_offset + align_up((size_t)B * pl.total_chunks * sizeof(uint64_t), 256);
   return pl;
 }
 
@@ -203,6 +206,8 @@ static int run_decode(const AttnParams* blocks, int n, cea_tensor* part_out, cea
   d.in_dtype = a.in_dtype;
   d.map = a.map;
   d.partial = (float*)ws;
+  d.vis = (uint16_t*)(ws + pl.vis_offset);
+  d.tile_mask = (uint64_t*)(ws + pl.mask_offset);
   d.G = a.Hq / a.Hkv;
   d.out = a.out; d.lse = a.lse;
   d.os_b = a.os_b; d.os_s = a.os_s; d.os_h = a.os_h;
@@ -214,6 +219,8 @@ static int run_decode(const AttnParams* blocks, int n, cea_tensor* part_out, cea
 
 static bool use_decode(const AttnParams& p) {
   if (!decode_supported(p.Sq, p.Hq, p.Hkv, p.D, p.in_dtype, p.map)) return false;
+  const int64_t sk = p.Sk;
+  if (plan_decode(&sk, 1, p.B, p.Sq, p.Hq, p.Hkv, p.D).total_chunks > kDecodeMaxChunks) return false;
   if (!(p.out_dtype == CEA_F32 || p.out_dtype == p.in_dtype)) return false;
   if (p.accumulate && p.out_dtype != CEA_F32) return false;
   if (!(fabs(p.scale) >= 1e-30 && fabs(p.scale) <= 1e30)) return false;
@@ -403,6 +410,7 @@ int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* 
       if (rc) return rc;
       dec = dec && use_decode(blocks[i]);
     }
+    dec = dec && plan_decode(sks, n, B, Sq, Hq, blocks[0].Hkv, D).total_chunks <= kDecodeMaxChunks;
     if (dec && part_out) {
       for (int i = 0; i < n && rc == 0; ++i) {
         rc = check_tensor(&part_out[i], "part_out", 4, acc, true);

@@ -71,8 +71,12 @@ struct DecodeParams {
   int32_t causal;
   int32_t in_dtype;
   HeadMap map;
-  // partial results [B, Hkv, total_chunks, G, Sq] x {D + 2} floats (o unnormalised, m, l)
+  // partial results [B, Hkv, total_chunks, NR rows (s, g)] x {D + 2} floats (o unnormalised,
+  // m, l); per-key visibility words [B, total_chunks, chunk] (bit s: query s sees the key);
+  // per-chunk masks [B, total_chunks] of 16-key tiles with a visible key
   float* partial;
+  uint16_t* vis;
+  uint64_t* tile_mask;
   int32_t G;                 // query heads per KV head handled by one work item
   // outputs of the reduction
   void* part_out[CEA_MAX_PARTS];   // optional per-partition (out, lse), f32
@@ -105,6 +109,7 @@ bool prefill_mfma_supported(const AttnParams& p);
 int launch_attn_prefill_mfma(const AttnParams& p, hipStream_t s);
 bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype,
                       const HeadMap& map);
+constexpr int kDecodeMaxChunks = 1024;  // key chunks per (batch, kv head), all partitions
 int decode_plan_chunk(int64_t total_keys, int32_t B, int32_t Hkv);
 int decode_rows(int32_t Sq, int32_t G);  // padded query rows per kv head, 0 = unsupported
 int launch_attn_decode(const DecodeParams& p, hipStream_t s);

@@ -36,6 +36,11 @@ __device__ __forceinline__ void buffer_load_lds16(i32x4 rs, const char* lds_base
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                ::"s"(lds_addr(lds_base)), "v"(voffset), "s"(rs) : "memory", "m0");
 }
+// Streaming variant (non-temporal): for data read once, such as a KV cache during decoding.
+__device__ __forceinline__ void buffer_load_lds16_nt(i32x4 rs, const char* lds_base, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               ::"s"(lds_addr(lds_base)), "v"(voffset), "s"(rs) : "memory", "m0");
+}
 // 4 bytes per lane (exact per-dword range check)
 __device__ __forceinline__ void buffer_load_lds4(i32x4 rs, const char* lds_base, uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
