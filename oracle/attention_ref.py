@@ -118,6 +118,13 @@ def empty_result(q: torch.Tensor, acc: torch.dtype):
     return torch.zeros(B, Sq, Hq, D, dtype=acc), torch.full((B, Hq, Sq), float("-inf"), dtype=acc)
 
 
+def empty_rows_fixup(o, l, mask):
+    """attention.py:173-176: the CPU flash op reports lse 0 for a row with no visible key;
+    such rows become out 0, lse -inf."""
+    empty = ~mask.any(dim=-1)
+    return o.masked_fill(empty.unsqueeze(-1), 0.0), l.masked_fill(empty, float("-inf"))
+
+
 def flash_lse(q, k, v, q_pos, k_pos, causal, scale, kv_map, acc):
     """attention.py:163-181: the CPU flash kernel over query chunks with an additive bias."""
     k, v, _ = _kv_for(k, v, q.shape[2], kv_map, native_gqa=True)
@@ -129,9 +136,7 @@ def flash_lse(q, k, v, q_pos, k_pos, causal, scale, kv_map, acc):
             bias = torch.zeros(mask.shape, dtype=acc).masked_fill(~mask, float("-inf"))
         o, l = _FLASH_CPU(qh[:, :, lo:hi], kh, vh, 0.0, mode == "causal", attn_mask=bias, scale=scale)
         if mask is not None:
-            empty = ~mask.any(dim=-1)
-            l = l.masked_fill(empty, float("-inf"))
-            o = o.masked_fill(empty.unsqueeze(-1), 0.0)
+            o, l = empty_rows_fixup(o, l, mask)
         outs.append(o)
         lses.append(l)
     out = outs[0] if len(outs) == 1 else torch.cat(outs, dim=2)

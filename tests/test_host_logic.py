@@ -1,0 +1,179 @@
+"""Host-side logic on the CPU: partitioning and layouts (known answers of the reference's
+tests/test_partition.py), the measured workloads' shapes and visible-pair counts (closed
+forms), and the oracle's per-rank sequence-parallel shares against single-device attention
+in f64 (the reference's tests/test_sequence_parallel.py:29-67, < 1e-12)."""
+
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+
+import _brute
+from oracle import attention_ref as ref
+from oracle import sp_ref
+
+cea = importlib.import_module("collaborative-edge-system_amd")
+P = cea.partition
+
+
+def test_split_sizes_known_answers():
+    """test_partition.py:13-29."""
+    assert P.split_sizes(12, 3) == [4, 4, 4]
+    assert P.split_sizes(10, 3) == [4, 3, 3]
+    assert P.split_sizes(12, [2, 1, 1]) == [6, 3, 3]
+    assert P.split_sizes(64, [0.7, 0.3], granularity=8) == [40, 24]
+    assert sum(P.split_sizes(1000, [5, 2, 0.1, 0.1])) == 1000
+    assert P.split_sizes(4, [100, 1, 1, 1]) == [1, 1, 1, 1]
+    assert min(P.split_sizes(10, [1000, 1])) >= 1
+    assert P.split_sizes(3, 5, min_units=0) == [1, 1, 1, 0, 0]
+    for bad in ((2, 3), (10, [1, -1])):
+        with pytest.raises(ValueError):
+            P.split_sizes(*bad)
+    with pytest.raises(ValueError):
+        P.split_sizes(10, 2, granularity=3)
+    assert P.offsets_of([3, 1, 2]) == [0, 3, 4]
+
+
+@pytest.mark.parametrize("hq,hkv,weights",
+                         [(8, 8, 2), (8, 4, 3), (8, 2, 4), (8, 1, 2), (6, 2, [3, 1]), (32, 8, [5, 2, 1]),
+                          (12, 4, 5), (64, 16, 8)])
+def test_partition_heads_is_consistent(hq, hkv, weights):
+    """test_partition.py:36-55."""
+    shards = P.partition_heads(hq, hkv, weights)
+    n = weights if isinstance(weights, int) else len(weights)
+    assert len(shards) == n and sum(s.q_count for s in shards) == hq
+    kv_of = P.default_kv_map(hq, hkv)
+    covered = []
+    for s in shards:
+        assert s.q_count >= 1 and s.kv_count >= 1
+        for i, local in enumerate(s.kv_map):
+            assert s.kv_start + local == kv_of[s.q_start + i]
+        covered.extend(range(s.q_start, s.q_start + s.q_count))
+    assert covered == list(range(hq))
+
+
+def test_partition_heads_avoids_replication_and_ulysses_share():
+    """test_partition.py:58-62; the 64/16-head model over 8 ranks gives 8 q / 2 kv heads per
+    rank with the regular local map (0,0,0,0,1,1,1,1)."""
+    assert [(s.kv_start, s.kv_count) for s in P.partition_heads(8, 4, 2)] == [(0, 2), (2, 2)]
+    assert all(s.kv_count == 1 and s.kv_start == 0 for s in P.partition_heads(8, 1, 2))
+    for s in P.partition_heads(64, 16, 8):
+        assert (s.q_count, s.kv_count) == (8, 2) and tuple(s.kv_map) == (0, 0, 0, 0, 1, 1, 1, 1)
+
+
+@pytest.mark.parametrize("kind", ["contiguous", "zigzag"])
+@pytest.mark.parametrize("seq_len,weights", [(11, [2, 1, 1]), (8, None), (5, [1, 1, 1, 1, 1]), (16, [1, 3])])
+def test_sequence_layout_roundtrip(kind, seq_len, weights):
+    """test_partition.py:65-79."""
+    n = len(weights) if weights else 2
+    layout = P.SequenceLayout(seq_len, n, weights, kind)
+    x = torch.arange(seq_len).view(1, seq_len, 1).repeat(2, 1, 3)
+    parts = [layout.shard(x, r) for r in range(n)]
+    assert [p.shape[1] for p in parts] == layout.sizes
+    assert torch.equal(layout.unshard(parts), x)
+    idx = torch.cat([layout.indices(r) for r in range(n)])
+    assert sorted(idx.tolist()) == list(range(seq_len))
+    for index in range(seq_len):
+        rank, local = layout.owner_of(index)
+        assert layout.indices(rank)[local].item() == index
+
+
+def test_zigzag_balances_causal_work():
+    """test_partition.py:82-86."""
+    layout = P.SequenceLayout(16, 4, kind="zigzag")
+    work = [int(layout.indices(r).sum()) + layout.sizes[r] for r in range(4)]
+    assert len(set(work)) == 1
+
+
+def test_ring_share_workload_pairs_closed_form():
+    """Zigzag share of rank 0 (sp=4, 32768 tokens): own block 4096*4097/2 + 4096^2 +
+    4096*4097/2 visible pairs; each other block is seen in full by the 4096 late queries."""
+    w = cea.workloads.ring_share(seq_len=32768, sp=4, rank=0, hq=1, hkv=1, d=8)
+    half = 4096 * 4097 // 2
+    assert w.pairs_per_step == [2 * half + 4096 * 4096] + [4096 * 8192] * 3
+    assert w.pairs_per_step == [33558528, 33554432, 33554432, 33554432]
+    assert w.ring_order == [0, 3, 2, 1]
+    assert w.flop == 4 * 8 * 1 * sum(w.pairs_per_step)
+    assert w.q_pos[0, 4095].item() == 4095 and w.q_pos[0, 4096].item() == 28672
+    # every rank of the zigzag layout has the same work
+    for r in range(1, 4):
+        assert sum(cea.workloads.ring_share(seq_len=32768, sp=4, rank=r, hq=1, hkv=1, d=8).pairs_per_step) \
+            == sum(w.pairs_per_step)
+
+
+def test_visible_pairs_matches_brute_count():
+    g = torch.Generator().manual_seed(3)
+    qp = torch.randint(-1, 50, (1, 40), generator=g)
+    kp = torch.randint(-1, 50, (1, 60), generator=g)
+    for causal in (True, False):
+        assert cea.workloads.visible_pairs(qp, kp, causal) == _brute.visible_count(qp, kp, causal)
+
+
+def test_kv_decode_workload_layout():
+    w = cea.workloads.kv_decode(batch=[0, 5])
+    assert w.part_sizes == [13107, 9830, 6554, 3277]
+    assert P.split_sizes(32768, [0.4, 0.3, 0.2, 0.1]) == w.part_sizes
+    for i, L in enumerate(w.lengths.tolist()):
+        assert 1024 <= L <= 32768
+        assert torch.equal(w.k_pos[i, :L], torch.arange(L)) and bool((w.k_pos[i, L:] == -1).all())
+        assert w.q_pos[i, 0].item() == L - 1
+        assert bool((w.cache_k[i, :, L:] == 0).all())
+    parts = w.partitions()
+    assert [p[0].shape[1] for p in parts] == w.part_sizes
+    assert parts[1][0].stride() == w.cache_k[:, :, 13107:].transpose(1, 2).stride()
+    # subsets draw the same rows as the full workload
+    w1 = cea.workloads.kv_decode(batch=[5])
+    assert torch.equal(w1.cache_k[0], w.cache_k[1]) and torch.equal(w1.q[0], w.q[1])
+
+
+def test_ulysses_workload_positions():
+    w = cea.workloads.ulysses_share(seq_len=4096)
+    L = sum(w.lengths)
+    assert L <= 4096 and w.q.shape == (1, 4096, 8, 128) and w.k.shape == (1, 4096, 2, 128)
+    assert torch.equal(w.pos[0, :L], torch.arange(L)) and bool((w.pos[0, L:] == -1).all())
+    assert w.kv_map == (0, 0, 0, 0, 1, 1, 1, 1)
+    assert w.flop == 4 * 128 * 8 * L * (L + 1) // 2
+
+
+# ---- the oracle's sequence-parallel shares == single-device attention (f64) -----------------
+
+B, S, HQ, HKV, D = 2, 13, 6, 3, 4
+
+
+def _inputs():
+    """tests/test_sequence_parallel.py:18-26 of the reference."""
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, S, HQ, D, generator=g, dtype=torch.float64)
+    k = torch.randn(B, S, HKV, D, generator=g, dtype=torch.float64)
+    v = torch.randn(B, S, HKV, D, generator=g, dtype=torch.float64)
+    pos = torch.arange(S).repeat(B, 1)
+    pos[1, :3] = -1
+    pos[1, 3:] -= 3
+    return q, k, v, pos
+
+
+@pytest.mark.parametrize("world,kind,weights,causal",
+                         [(2, "contiguous", None, True), (2, "zigzag", None, True),
+                          (3, "zigzag", [3, 2, 1], True), (3, "contiguous", [1, 2, 3], False)])
+def test_oracle_shares_match_single_device(world, kind, weights, causal):
+    q, k, v, pos = _inputs()
+    full = ref.plain_attention(q, k, v, pos, pos, causal=causal)
+    layout = P.SequenceLayout(S, world, weights, kind)
+    blocks = [(layout.shard(k, r), layout.shard(v, r), layout.shard(pos, r)) for r in range(world)]
+    ring = [sp_ref.ring_share(layout.shard(q, r), layout.shard(pos, r), blocks, r, causal=causal)
+            for r in range(world)]
+    valid = pos >= 0
+    assert (layout.unshard(ring) - full)[valid].abs().max().item() < 1e-12
+    dkv = sp_ref.distributed_kv_share(q[:, -2:], pos[:, -2:], blocks, causal=causal)
+    assert (dkv - full[:, -2:]).abs().max().item() < 1e-12
+    # Ulysses: every rank's heads over the whole sequence
+    for sh in P.partition_heads(HQ, HKV, weights or world):
+        qs, ks = q[:, :, sh.q_start:sh.q_start + sh.q_count], k[:, :, sh.kv_start:sh.kv_start + sh.kv_count]
+        vs = v[:, :, sh.kv_start:sh.kv_start + sh.kv_count]
+        out = sp_ref.ulysses_local(qs, ks, vs, pos, sh.kv_map, causal=causal)
+        assert (out - full[:, :, sh.q_start:sh.q_start + sh.q_count])[valid].abs().max().item() < 1e-12
+    # the brute force agrees with the single-device result too
+    bo, _ = _brute.attention(q, k, v, pos, pos, causal)
+    assert (torch.from_numpy(bo) - full)[valid].abs().max().item() < 1e-12

@@ -1,0 +1,229 @@
+"""Pins of the layer-op oracle (oracle/layers_ref.py) on the CPU.
+
+* f64: closed forms written independently of the oracle - RMSNorm per row with numpy
+  (the reference's tests/reference.py:17-18), rotary as a complex rotation of the pairs
+  (x[i], x[i + D/2]) (half-split, tests/reference.py:21-29), inv_freq = theta^(-2i/D), SiLU as
+  g / (1 + exp(-g)); all to 1e-12.
+* bf16: the reference rounds at fixed points (llama.py:59-61, 76-77, 87-88, 305).  The
+  oracle's bf16 results are compared with the same rounding points applied by an
+  independent numpy round-to-nearest-even to the fp64 closed forms: equal except for rare
+  last-bit differences of the f32 intermediate (<= 0.5% of elements, never more than one
+  bf16 ulp).  A single fused rounding, the classic mistake of a fused kernel, is shown to
+  differ in far more elements.
+* planted mistakes (interleaved rotary pairs, exponent i/D, missing gate factor, fused
+  rounding) are swapped into the oracle and rejected.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import layers_ref as L
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """fp64 -> f32 -> bf16 (round to nearest even on the upper 16 bits), returned as fp64."""
+    f = np.asarray(x, dtype=np.float32)
+    bits = f.view(np.uint32).astype(np.uint64)
+    bits = (bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000
+    return bits.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def ulp_bf16(x: np.ndarray) -> np.ndarray:
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---- RMSNorm ------------------------------------------------------------------------------
+
+def _rms_closed(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    out = np.empty_like(x)
+    for r in range(x.shape[0]):
+        row = x[r]
+        out[r] = w * (row / math.sqrt(float(np.dot(row, row)) / row.size + eps))
+    return out
+
+
+def test_rmsnorm_f64_closed_form():
+    x = torch.randn(64, 256, generator=_gen(0), dtype=torch.float64)
+    w = 1 + 0.02 * torch.randn(256, generator=_gen(1), dtype=torch.float64)
+    y = L.rmsnorm(x, w, 1e-5).numpy()
+    assert np.abs(y - _rms_closed(x.numpy(), w.numpy(), 1e-5)).max() <= 1e-12
+
+
+def _rms_rounding_points(x, w, eps):
+    """bf16(w * bf16(norm)) with norm from the fp64 closed form."""
+    xn = x.double().numpy()
+    norm = xn / np.sqrt((xn * xn).mean(-1, keepdims=True) + eps)
+    return bf16_round(w.double().numpy() * bf16_round(norm))
+
+
+def test_rmsnorm_bf16_rounding_points():
+    x = torch.randn(256, 4096, generator=_gen(2)).to(torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(4096, generator=_gen(3))).to(torch.bfloat16)
+    y = L.rmsnorm(x, w, 1e-5).double().numpy()
+    want = _rms_rounding_points(x, w, 1e-5)
+    diff = np.abs(y - want)
+    assert (diff <= ulp_bf16(want) * 1.0001).all()
+    assert (diff > 0).mean() <= 5e-3
+    # a single rounding of the f32 product misses the reference's intermediate rounding
+    xn = x.double().numpy()
+    fused = bf16_round(w.double().numpy() * xn / np.sqrt((xn * xn).mean(-1, keepdims=True) + 1e-5))
+    assert (fused != want).mean() > 2e-2
+
+
+def test_planted_fused_rounding_is_caught(monkeypatch):
+    def fused(x, weight, eps):
+        h = x.float()
+        h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
+        return (weight.float() * h).to(x.dtype)
+
+    monkeypatch.setattr(L, "rmsnorm", fused)
+    with pytest.raises(AssertionError):
+        test_rmsnorm_bf16_rounding_points()
+
+
+# ---- rotary ---------------------------------------------------------------------------------
+
+def test_inv_freq_closed_form():
+    for D, theta in ((128, 1e4), (64, 5e5), (8, 10.0)):
+        inv = L.inv_freq(D, theta).double().numpy()
+        want = np.array([theta ** (-2.0 * i / D) for i in range(D // 2)])
+        assert np.abs(inv / want - 1).max() <= 2.0 ** -22
+        inv64 = L.inv_freq(D, theta, dtype=torch.float64).numpy()
+        assert np.abs(inv64 / want - 1).max() <= 1e-14
+    lin = L.inv_freq(128, 1e4, {"rope_type": "linear", "factor": 4.0}, dtype=torch.float64).numpy()
+    assert np.allclose(lin, L.inv_freq(128, 1e4, dtype=torch.float64).numpy() / 4, rtol=1e-15)
+
+
+def test_llama3_scaling_regimes():
+    """Llama 3.1 frequency scaling: wavelengths below original/high_freq_factor unchanged,
+    above original/low_freq_factor divided by factor, smooth and monotone in between."""
+    sc = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+    base = L.inv_freq(128, 5e5, dtype=torch.float64).numpy()
+    got = L.inv_freq(128, 5e5, sc, dtype=torch.float64).numpy()
+    wl = 2 * math.pi / base
+    hi = wl < 8192 / 4.0
+    lo = wl > 8192 / 1.0
+    assert np.allclose(got[hi], base[hi], rtol=1e-15)
+    assert np.allclose(got[lo], base[lo] / 8, rtol=1e-15)
+    mid = ~hi & ~lo
+    assert mid.any()
+    ratio = got[mid] / base[mid]
+    assert ((ratio <= 1) & (ratio >= 1 / 8)).all() and (np.diff(ratio) <= 0).all()
+    with pytest.raises(NotImplementedError):
+        L.inv_freq(128, 1e4, {"rope_type": "yarn", "factor": 2.0})
+
+
+def _rope_complex(x: np.ndarray, pos: np.ndarray, inv: np.ndarray) -> np.ndarray:
+    """x [S, H, D]: pairs (x[i], x[i + D/2]) as complex numbers times exp(i * pos * inv[i])."""
+    h = x.shape[-1] // 2
+    z = x[..., :h] + 1j * x[..., h:]
+    ang = np.maximum(pos, 0)[:, None, None] * inv[None, None, :]
+    r = z * np.exp(1j * ang)
+    return np.concatenate([r.real, r.imag], axis=-1)
+
+
+def test_rotary_f64_is_a_rotation_of_half_split_pairs():
+    S, H, D = 33, 3, 16
+    x = torch.randn(1, S, H, D, generator=_gen(4), dtype=torch.float64)
+    pos = torch.arange(S).view(1, S) - 2  # two padding positions clamp to angle 0
+    inv = L.inv_freq(D, 1e4, dtype=torch.float64)
+    cos, sin = L.rope_tables(pos, inv, torch.float64)
+    y = L.apply_rotary(x, cos, sin)[0].numpy()
+    want = _rope_complex(x[0].numpy(), pos[0].numpy(), inv.numpy())
+    assert np.abs(y - want).max() <= 1e-12
+    # norms of the pairs are preserved; padding rows are untouched
+    assert np.allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x[0].numpy(), axis=-1))
+    assert np.array_equal(y[:3], x[0].numpy()[:3])
+
+
+def test_planted_interleaved_pairs_are_caught(monkeypatch):
+    def interleaved(x):
+        out = torch.empty_like(x)
+        out[..., 0::2] = -x[..., 1::2]
+        out[..., 1::2] = x[..., 0::2]
+        return out
+
+    monkeypatch.setattr(L, "rotate_half", interleaved)
+    with pytest.raises(AssertionError):
+        test_rotary_f64_is_a_rotation_of_half_split_pairs()
+
+
+def test_planted_exponent_is_caught(monkeypatch):
+    good = L.inv_freq
+
+    def wrong(head_dim, theta, scaling=None, dtype=torch.float32):
+        return good(2 * head_dim, theta, scaling, dtype)[: head_dim // 2]
+
+    monkeypatch.setattr(L, "inv_freq", wrong)
+    with pytest.raises(AssertionError):
+        test_inv_freq_closed_form()
+
+
+def test_rotary_bf16_rounding_points():
+    """bf16 tables from f32 angles; x*cos, rot*sin and their sum each rounded to bf16."""
+    S, H, D = 512, 4, 128
+    x = torch.randn(1, S, H, D, generator=_gen(5)).to(torch.bfloat16)
+    pos = torch.arange(S).view(1, S)
+    inv = L.inv_freq(D, 1e4)
+    cos, sin = L.rope_tables(pos, inv, torch.bfloat16)
+    ang = (pos[0].float()[:, None] * inv[None, :]).double().numpy()  # one f32 multiply
+    ang = np.concatenate([ang, ang], axis=-1)
+    c, s = bf16_round(np.cos(ang)), bf16_round(np.sin(ang))
+    assert np.abs(cos[0].double().numpy() - c).max() <= ulp_bf16(c).max()
+    assert (cos[0].double().numpy() != c).mean() <= 5e-3
+    xn = x[0].double().numpy()
+    rot = np.concatenate([-xn[..., D // 2:], xn[..., :D // 2]], axis=-1)
+    cc, ss = cos[0].double().numpy()[:, None, :], sin[0].double().numpy()[:, None, :]
+    want = bf16_round(bf16_round(xn * cc) + bf16_round(rot * ss))
+    y = L.apply_rotary(x, cos, sin)[0].double().numpy()
+    assert np.array_equal(y, want)
+
+
+# ---- SiLU gate ------------------------------------------------------------------------------
+
+def test_silu_gate_f64_closed_form():
+    g = torch.randn(64, 300, generator=_gen(6), dtype=torch.float64) * 4
+    u = torch.randn(64, 300, generator=_gen(7), dtype=torch.float64)
+    gn, un = g.numpy(), u.numpy()
+    want = gn / (1 + np.exp(-gn)) * un
+    assert np.abs(L.silu_gate(g, u).numpy() - want).max() <= 1e-12
+
+
+def test_silu_gate_bf16_rounding_points():
+    g = torch.randn(512, 1024, generator=_gen(8)).to(torch.bfloat16)
+    u = torch.randn(512, 1024, generator=_gen(9)).to(torch.bfloat16)
+    gn, un = g.double().numpy(), u.double().numpy()
+    want = bf16_round(bf16_round(gn / (1 + np.exp(-gn))) * un)
+    y = L.silu_gate(g, u).double().numpy()
+    diff = np.abs(y - want)
+    assert (diff <= ulp_bf16(want) * 1.0001).all()
+    assert (diff > 0).mean() <= 5e-3
+
+
+def test_planted_missing_gate_factor_is_caught(monkeypatch):
+    monkeypatch.setattr(L, "silu_gate", lambda g, u: torch.sigmoid(g) * u)
+    with pytest.raises(AssertionError):
+        test_silu_gate_f64_closed_form()
+
+
+def test_rmsnorm_rope_f64_composition():
+    S, H, D = 17, 4, 32
+    x = torch.randn(S, H * D, generator=_gen(10), dtype=torch.float64)
+    w = 1 + 0.02 * torch.randn(H * D, generator=_gen(11), dtype=torch.float64)
+    pos = torch.arange(S)
+    inv = L.inv_freq(D, 1e4, dtype=torch.float64)
+    y = L.rmsnorm_rope(x, w, 1e-5, pos, inv, H)[0].numpy()
+    normed = _rms_closed(x.numpy(), w.numpy(), 1e-5).reshape(S, H, D)
+    want = _rope_complex(normed, pos.numpy(), inv.numpy())
+    assert np.abs(y - want).max() <= 1e-12
