@@ -1,0 +1,168 @@
+"""GPU parity of the layer-op kernels (RMSNorm, rotary tables, rotary, fused RMSNorm+rotary,
+SiLU gate) against the CPU oracle, through the C ABI.
+
+Tolerances (written here, used below):
+* bf16: every element within one bf16 ulp of the oracle (the oracle rounds at the
+  reference's points, so only a last-bit difference of a transcendental or an f32
+  intermediate can remain), at most 1e-3 of the elements differing at all, and
+  max |diff| <= 2e-2 over elements with |ref| < 2 (the workload's absolute bound; above 2 a
+  single ulp is larger than 2e-2, and the ulp bound applies).  For RMSNorm followed by
+  rotary, a last-bit flip of the normalised value y propagates through x*cos + rot*sin,
+  whose sum may be much smaller than its terms: there the bound is two ulps of the larger
+  term magnitude max(|y_i|, |y_j|) of the rotated pair, with the same 1e-3 and 2e-2 rules
+  on that magnitude;
+* f32: normwise rel <= 1e-6;  f64: max abs <= 1e-12.
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from oracle import layers_ref as L
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    e = torch.floor(torch.log2(x.abs().clamp(min=2.0 ** -126)))
+    return torch.exp2(e - 7)
+
+
+def assert_close_layer(y: torch.Tensor, ref: torch.Tensor, what: str, mag: torch.Tensor = None,
+                       ulps: float = 1.0):
+    """``mag``: magnitude the bf16 ulp bound is taken from (default |ref|)."""
+    y = y.detach().cpu()
+    assert y.shape == ref.shape and y.dtype == ref.dtype, (what, y.shape, ref.shape, y.dtype, ref.dtype)
+    if y.dtype == torch.float64:
+        err = (y - ref).abs().max().item()
+        assert err <= 1e-12, f"{what}: {err:.3e}"
+        return
+    if y.dtype == torch.float32:
+        err = (y - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+        assert err <= 1e-6, f"{what}: rel {err:.3e}"
+        return
+    a, b = y.float(), ref.float()
+    m = b.abs() if mag is None else mag.float().abs()
+    diff = (a - b).abs()
+    assert torch.isfinite(a).all(), f"{what}: non-finite values"
+    over = diff > _ulp_bf16(m) * ulps * 1.0001
+    assert not over.any(), f"{what}: {int(over.sum())} elements beyond {ulps} bf16 ulp, max {diff.max().item():.3e}"
+    frac = (diff > 0).float().mean().item()
+    assert frac <= 1e-3, f"{what}: {frac:.2e} of the elements differ"
+    small = m < 2
+    if small.any():
+        assert diff[small].max().item() <= 2e-2, what
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+@pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (4096, 4096)), (torch.float32, (64, 1000)),
+                                         (torch.float64, (8, 300)), (torch.float16, (33, 512))])
+def test_rmsnorm(cea, dev, dtype, shape):
+    x = torch.randn(*shape, generator=_gen(0)).to(dtype)
+    w = (1 + 0.02 * torch.randn(shape[-1], generator=_gen(1))).to(dtype)
+    y = cea.layers.rmsnorm(x.to(dev), w.to(dev), 1e-5)
+    torch.cuda.synchronize()
+    assert_close_layer(y, L.rmsnorm(x, w, 1e-5), f"rmsnorm {dtype}")
+
+
+def test_rmsnorm_module_mixed_dtypes_and_views(cea, dev):
+    """A f32 weight on bf16 activations promotes (llama.py:61); non-contiguous rows."""
+    x = torch.randn(3, 40, 256, generator=_gen(2)).to(torch.bfloat16)
+    w = 1 + 0.02 * torch.randn(256, generator=_gen(3))
+    y = cea.layers.rmsnorm(x.to(dev), w.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert_close_layer(y, L.rmsnorm(x, w, 1e-6), "rmsnorm promoted")
+    big = torch.randn(40, 512, generator=_gen(4)).to(torch.bfloat16)
+    view = big[:, 128:384]  # row stride 512
+    m = cea.RMSNorm(256, 1e-5, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    assert_close_layer(m(view.to(dev)), L.rmsnorm(view, torch.ones(256, dtype=torch.bfloat16), 1e-5),
+                       "rmsnorm view")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float64])
+def test_rope_tables_and_rotary(cea, dev, dtype):
+    S, H, D = 4096, 32, 128
+    pos = torch.arange(S).view(1, S)
+    pos[0, :5] = -1  # padding: angle 0
+    inv = L.inv_freq(D, 1e4, dtype=torch.float64 if dtype == torch.float64 else torch.float32)
+    cos, sin = cea.layers.rope_tables(pos.to(dev), inv.to(dev), dtype)
+    rc, rs = L.rope_tables(pos, inv, dtype)
+    x = torch.randn(1, S, H, D, generator=_gen(5)).to(dtype)
+    y = cea.layers.apply_rotary(x.to(dev), cos, sin)
+    torch.cuda.synchronize()
+    assert_close_layer(cos, rc, "cos")
+    assert_close_layer(sin, rs, "sin")
+    # rotary on the kernel's own tables vs the oracle on the same tables
+    assert_close_layer(y, L.apply_rotary(x, cos.cpu(), sin.cpu()), "apply_rotary")
+
+
+def test_rotary_embedding_module_llama3_scaling(cea, dev):
+    cfg = SimpleNamespace(head_dim=64, rope_theta=5e5,
+                          rope_scaling={"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                                        "high_freq_factor": 4.0, "original_max_position_embeddings": 8192})
+    rot = cea.RotaryEmbedding(cfg, device=dev)
+    pos = torch.arange(0, 20000, 7).view(1, -1)
+    cos, sin = rot(pos.to(dev), torch.float32)
+    inv = L.inv_freq(64, 5e5, cfg.rope_scaling)
+    rc, rs = L.rope_tables(pos, inv, torch.float32)
+    torch.cuda.synchronize()
+    # f32 tables: the angle is one f32 multiply in both; cos/sin of large angles differ by
+    # the f32 rounding of the argument reduction, bounded here absolutely
+    assert (cos.cpu() - rc).abs().max().item() <= 2e-6
+    assert (sin.cpu() - rs).abs().max().item() <= 2e-6
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rmsnorm_rope_fused(cea, dev, dtype):
+    """RMSNorm [4096, 4096] then rotary on the [1, 4096, 32, 128] view at positions 0..4095."""
+    S, H, D = 4096, 32, 128
+    x = torch.randn(S, H * D, generator=_gen(6)).to(dtype)
+    w = (1 + 0.02 * torch.randn(H * D, generator=_gen(7))).to(dtype)
+    pos = torch.arange(S)
+    inv = L.inv_freq(D, 1e4)
+    y = cea.rmsnorm_rope(x.to(dev), w.to(dev), 1e-5, pos.to(dev), inv.to(dev), H)
+    torch.cuda.synchronize()
+    normed = L.rmsnorm(x, w, 1e-5).view(1, S, H, D).float()
+    pair = torch.maximum(normed.abs(), L.rotate_half(normed).abs())
+    assert_close_layer(y, L.rmsnorm_rope(x, w, 1e-5, pos, inv, H), f"rmsnorm_rope {dtype}",
+                       mag=pair, ulps=2.0)
+
+
+@pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (4096, 14336)), (torch.float32, (100, 3000)),
+                                         (torch.float64, (10, 77))])
+def test_silu_mul(cea, dev, dtype, shape):
+    g = torch.randn(*shape, generator=_gen(8)).to(dtype)
+    u = torch.randn(*shape, generator=_gen(9)).to(dtype)
+    y = cea.silu_mul(g.to(dev), u.to(dev))
+    torch.cuda.synchronize()
+    assert_close_layer(y, L.silu_gate(g, u), f"silu_mul {dtype}")
+
+
+def test_silu_mul_on_fused_gemm_halves(cea, dev):
+    """gate/up as column halves of one [T, 2I] GEMM output (row stride 2I)."""
+    fused = torch.randn(512, 2 * 1000, generator=_gen(10)).to(torch.bfloat16)
+    g, u = fused[:, :1000], fused[:, 1000:]
+    fd = fused.to(dev)
+    y = cea.layers.gated_activation("silu")(fd[:, :1000], fd[:, 1000:])
+    torch.cuda.synchronize()
+    assert_close_layer(y, L.silu_gate(g, u), "silu halves")
+
+
+def test_layer_errors(cea, dev):
+    x = torch.randn(4, 100, device=dev)
+    with pytest.raises(ValueError):
+        cea.rmsnorm_rope(x, torch.ones(100, device=dev), 1e-5, torch.arange(4, device=dev),
+                         torch.ones(4, device=dev), 3)
+    with pytest.raises(ValueError):
+        cea.silu_mul(x, torch.randn(4, 99, device=dev))
+    with pytest.raises(NotImplementedError):
+        cea.layers.gated_activation("gelu_new")
+    with pytest.raises(RuntimeError):
+        cea.silu_mul(x.cpu(), x.cpu())  # host tensors are refused, never computed on the CPU
