@@ -35,6 +35,18 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def _measured_traffic(name: str):
+    """HBM bytes per launch of a kernel, from the FETCH_SIZE / WRITE_SIZE counter runs
+    summarised in profiles/<name>_pmc.md (line ``traffic_bytes_per_launch: N``), or None."""
+    path = ROOT / "profiles" / f"{name}_pmc.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def _timed(fn, steps: int, warmup: int, torch):
     for _ in range(warmup):
         fn()
@@ -82,7 +94,7 @@ def bench_ring(cea, torch, steps, warmup, dev):
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": None,
+        "traffic": _measured_traffic("attn_prefill_ring_share"),
         "kernel": "attn_prefill_kernel<bf16,128> (+ tile summary pass), one ring step",
         "launch_ms": round(launch_ms, 4),
         "flop_per_launch": int(flop_launch),
@@ -162,7 +174,8 @@ def cpu_baseline(cea, torch, budget_s: float = 20.0):
     from oracle import sp_ref
 
     w = cea.workloads.ring_share(device="cpu")
-    threads = os.cpu_count() or 1
+    # the host share of one GPU: OMP_NUM_THREADS where set, else at most 16 cores
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
     half = w.q.shape[1] // 2
     rows, done_s, done_flop, sample = 64, 0.0, 0, []
@@ -217,9 +230,10 @@ def main() -> int:
     only = set(filter(None, args.only.split(",")))
     want = lambda name: not only or name in only  # noqa: E731
 
-    result = {}
-    _log("ring share (headline)")
-    w, sec, tflops, roof = bench_ring(cea, torch, args.steps, args.warmup, dev)
+    w = sec = tflops = roof = None
+    if want("ring"):
+        _log("ring share (headline)")
+        w, sec, tflops, roof = bench_ring(cea, torch, args.steps, args.warmup, dev)
     secondary = {}
     if want("decode"):
         _log("distributed-KV decode")
@@ -239,12 +253,12 @@ def main() -> int:
 
     result = {
         "metric": "attn prefill TFLOP/s (% MFMA peak); decode+merge GB/s (% HBM peak)",
-        "value": round(tflops, 2),
+        "value": round(tflops, 2) if w else None,
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(sec * 1e3, 4),
+        "ms_per_step": round(sec * 1e3, 4) if w else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -253,9 +267,9 @@ def main() -> int:
         "config": {
             "workload": "ring_attention share: rank 0 of sp=4 zigzag, 32768 tokens, GQA 32/8, "
                         "D=128, bf16, q 8192 x 4 KV blocks of 8192, online f32 merge",
-            "frac_of_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
-            "flop_per_step": w.flop,
-            "visible_pairs_per_step": w.pairs_per_step,
+            "frac_of_peak": round(tflops / PEAK_BF16_TFLOPS, 4) if w else None,
+            "flop_per_step": w.flop if w else None,
+            "visible_pairs_per_step": w.pairs_per_step if w else None,
             "parallelism": "single GPU, simulated ring (no collectives)",
         },
         "roofline": roof,
