@@ -268,30 +268,49 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
       for (int ks = 0; ks < D / 16; ++ks) acc = Mfma<T>::run(kf[ks], qf[ks], acc);
       sacc[kb] = acc;
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, D / 16, 0);
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, D / 16, 0);
     if (mode == 2) {
+      // key visible: it exists (key < left) and, read as unsigned, k_pos <= q_pos (causal;
+      // -1 wraps to the maximum) or k_pos >= 0 (not causal); a padded query row sees
+      // nothing when causal
       const char* pl = sb + L::K_BYTES + L::V_BYTES;
       const int left = p.Sk - t * BN;
+      const bool row_sees = p.causal ? (row_ok && qpos >= 0) : row_ok;
+      const uint64_t qlim = p.causal ? (uint64_t)qpos : (uint64_t)INT64_MAX;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
+          const int key0 = kb * 32 + i4 * 8 + g * 4;
+          const uint4 a = *(const uint4*)(pl + key0 * 8);        // keys key0, key0 + 1
+          const uint4 a2 = *(const uint4*)(pl + key0 * 8 + 16);  // keys key0 + 2, key0 + 3
+          const uint64_t kp[4] = {((uint64_t)a.y << 32) | a.x, ((uint64_t)a.w << 32) | a.z,
+                                  ((uint64_t)a2.y << 32) | a2.x, ((uint64_t)a2.w << 32) | a2.z};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int key = kb * 32 + i4 * 8 + g * 4 + j;
-            const int64_t kp = *(const int64_t*)(pl + key * 8);
-            const bool vis = row_ok && key < left && kp >= 0 && (!p.causal || kp <= qpos);
+            const bool vis = row_sees && key0 + j < left && kp[j] <= qlim;
             if (!vis) sacc[kb][i4 * 4 + j] = -__builtin_inff();
           }
         }
     }
     // online softmax (exp2 domain) with a lazily moved reference maximum
-    float mx = max3f(sacc[0][0], sacc[0][1], sacc[0][2]);
+    // row maximum as a tree of independent max3 (short dependency chains)
+    float t1[11];
 #pragma unroll
-    for (int e = 3; e < 15; e += 2) mx = max3f(mx, sacc[0][e], sacc[0][e + 1]);
-    mx = max3f(mx, sacc[0][15], sacc[1][0]);
-#pragma unroll
-    for (int e = 1; e < 15; e += 2) mx = max3f(mx, sacc[1][e], sacc[1][e + 1]);
-    mx = __builtin_fmaxf(mx, sacc[1][15]);
+    for (int i = 0; i < 10; ++i) {
+      const int e = 3 * i;
+      t1[i] = max3f(sacc[e >> 4][e & 15], sacc[(e + 1) >> 4][(e + 1) & 15], sacc[(e + 2) >> 4][(e + 2) & 15]);
+    }
+    t1[10] = __builtin_fmaxf(sacc[1][14], sacc[1][15]);
+    const float t2a = max3f(t1[0], t1[1], t1[2]), t2b = max3f(t1[3], t1[4], t1[5]);
+    const float t2c = max3f(t1[6], t1[7], t1[8]), t2d = __builtin_fmaxf(t1[9], t1[10]);
+    float mx = __builtin_fmaxf(max3f(t2a, t2b, t2c), t2d);
     mx = max_halves(mx);
     const bool grow = mx > m_run + grow_thr;
     if (__ballot(grow) != 0) {
@@ -305,17 +324,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
     }
-    float psum = 0.f;
     frag pf[4];
+    float pr[32];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][e], c, -m_use));
-        psum += pv;
-        pf[kb * 2 + (e >> 3)][e & 7] = (T)pv;
+        pr[kb * 16 + e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][e], c, -m_use));
+        pf[kb * 2 + (e >> 3)][e & 7] = (T)pr[kb * 16 + e];
       }
-    l_run += psum;
+    // f32 row sum as a tree of independent adds
+#pragma unroll
+    for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+      for (int e = 0; e < w; ++e) pr[e] += pr[e + w];
+    l_run += pr[0];
     // O^T += V^T . P^T: fragment of step s holds keys s*16 + {g*4..+3, 8+g*4..+3}
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
@@ -327,6 +350,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
 #pragma unroll
       for (int s = 0; s < 4; ++s) oacc[dt] = Mfma<T>::run(vf[s], pf[s], oacc[dt]);
     }
+    // the transposing reads of the next 16 columns overlap the products of these
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+#pragma unroll
+    for (int j = 0; j < D / 32 - 1; ++j) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
   };
 
   // ---- passes over the key block: list the tiles this workgroup needs, then stream them

@@ -47,6 +47,16 @@ __device__ __forceinline__ void buffer_load_lds4(i32x4 rs, const char* lds_base,
                ::"s"(lds_addr(lds_base)), "v"(voffset), "s"(rs) : "memory", "m0");
 }
 
+// The same loads with the LDS destination given as an LDS byte address (wave-uniform).
+__device__ __forceinline__ void buffer_load_lds16_m0(i32x4 rs, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(rs) : "memory", "m0");
+}
+__device__ __forceinline__ void buffer_load_lds4_m0(i32x4 rs, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(rs) : "memory", "m0");
+}
+
 // Waits until at most N of this wave's vector-memory loads are outstanding.
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
