@@ -47,6 +47,10 @@ FILE_FLAGS = {
     # M0 is set by the kernel's own LDS-DMA assembly; the clobber note is expected
     "attn_prefill.hip": ["-fno-honor-nans", "-Wno-inline-asm"],
     "attn_decode.hip": ["-fno-honor-nans", "-Wno-inline-asm"],
+    # the layer ops round every product to the tensor dtype before the next add, as the
+    # reference's separate tensor ops do: no multiply-add contraction (without this flag
+    # x*cos + rot*sin in f16 becomes an f16 fma, and f32 products fuse into the sums)
+    "layers.hip": ["-ffp-contract=off"],
 }
 
 

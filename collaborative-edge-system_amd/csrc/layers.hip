@@ -50,6 +50,22 @@ __device__ __forceinline__ void store_vec(T* p, const T (&in)[VEC]) {
   }
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Non-temporal store for output written exactly once (streamed past the caches; measured
+// faster than plain stores for the row and elementwise passes here, while their loads are
+// fastest as plain loads); 16-byte vectors only, plain stores otherwise.
+template <typename T, int VEC>
+__device__ __forceinline__ void store_vec_stream(T* p, const T (&in)[VEC]) {
+  if constexpr (VEC * sizeof(T) == 16) {
+    u32x4_t raw;
+    __builtin_memcpy(&raw, in, 16);
+    __builtin_nontemporal_store(raw, (u32x4_t*)p);
+  } else {
+    store_vec<T, VEC>(p, in);
+  }
+}
+
 template <typename T> struct math_of { typedef float type; };
 template <> struct math_of<double> { typedef double type; };
 
@@ -198,7 +214,8 @@ __device__ __forceinline__ void rotate_pair(const T (&x1)[VEC], const T (&x2)[VE
     const M a1 = widen<T, M>(x1[e]), a2 = widen<T, M>(x2[e]);
     // first half: x1*cos + (-x2)*sin ; second half: x2*cos + x1*sin
     const M p1 = rnd<T, M>(mul_rn(a1, widen<T, M>(c1[e])));
-    const M q1 = rnd<T, M>(mul_rn(-a2, widen<T, M>(s1[e])));
+    // (-x2)*sin rounds to the negation of x2*sin (round-to-nearest-even is symmetric)
+    const M q1 = -rnd<T, M>(mul_rn(a2, widen<T, M>(s1[e])));
     const M p2 = rnd<T, M>(mul_rn(a2, widen<T, M>(c2[e])));
     const M q2 = rnd<T, M>(mul_rn(a1, widen<T, M>(s2[e])));
     o1[e] = narrow<T, M>(add_rn(p1, q1));
@@ -305,6 +322,106 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(
   }
 }
 
+// Single-pass variant for rows of at most 256 feature-pair chunks (e.g. 32 heads x 128) and
+// D <= 512: a block takes R consecutive rows and every thread owns the same VEC-wide pair
+// chunk (j, j + D/2 of one head) of each of them, in the sum of squares and in the output.
+// x is read from memory once and kept in registers, the weight chunk is loaded once for the
+// R rows, and the output is written non-temporally (measured: plain loads with streaming
+// stores beat every other combination for this read-once, write-once row pass).  The position and frequency loads of the
+// rotary table entries are issued ahead of the row loads (loads complete in order), so
+// the table evaluation overlaps the row loads instead of waiting behind them.
+template <typename T, int VEC, int R>
+__global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
+    const T* __restrict__ x, int64_t xs, const T* __restrict__ w, const int64_t* __restrict__ pos,
+    int64_t ps, const typename math_of<T>::type* __restrict__ inv_freq, T* __restrict__ out,
+    int64_t os, int64_t S, int H, int D, double eps_d) {
+  typedef typename math_of<T>::type M;
+  static_assert(VEC * sizeof(T) == 16, "16-byte chunks");
+  constexpr int TE = (R * 256 + 255) / 256;  // table entries per thread (half <= 256)
+  __shared__ M red[R][4];
+  __shared__ T tab_c[R][256];
+  __shared__ T tab_s[R][256];
+  const int64_t row0 = (int64_t)blockIdx.x * R;
+  const int C = H * D;
+  const int half = D / 2;
+  const int nch = half / VEC;
+  const int it = threadIdx.x;
+  const bool active = it < H * nch;
+  const int h = active ? it / nch : 0;
+  const int j = active ? (it % nch) * VEC : 0;
+  const int c1 = h * D + j, c2 = c1 + half;
+
+  M ang[TE];
+#pragma unroll
+  for (int k = 0; k < TE; ++k) {
+    const int t = threadIdx.x + 256 * k;
+    const int r = t / half, jj = t - r * half;
+    ang[k] = (t < R * half && row0 + r < S) ? mul_rn(pos_to<M>(pos[(row0 + r) * ps]), inv_freq[jj])
+                                           : (M)0;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  T x1[R][VEC], x2[R][VEC], w1[VEC], w2[VEC];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (active && row0 + r < S) {
+      const T* xr = x + (row0 + r) * xs;
+      load_vec<T, VEC>(xr + c1, x1[r]);
+      load_vec<T, VEC>(xr + c2, x2[r]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x1[r][e] = x2[r][e] = T(0);
+    }
+  }
+  if (active) {
+    load_vec<T, VEC>(w + c1, w1);
+    load_vec<T, VEC>(w + c2, w2);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < TE; ++k) {
+    const int t = threadIdx.x + 256 * k;
+    const int r = t / half, jj = t - r * half;
+    if (t < R * half) {
+      M sv, cv;
+      sincos_acc(ang[k], &sv, &cv);
+      tab_c[r][jj] = narrow<T, M>(cv);
+      tab_s[r][jj] = narrow<T, M>(sv);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    M acc = 0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const M a = widen<T, M>(x1[r][e]), b = widen<T, M>(x2[r][e]);
+      acc += a * a;
+      acc += b * b;
+    }
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) red[r][threadIdx.x >> 6] = acc;
+  }
+  __syncthreads();  // publishes the partial sums and the tables
+  if (!active) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (row0 + r >= S) break;
+    const M ss = red[r][0] + red[r][1] + red[r][2] + red[r][3];
+    const M rs = rsqrt_rn(add_rn(div_rn(ss, (M)C), (M)eps_d));
+    T y1[VEC], y2[VEC], cs[VEC], sn[VEC], o1[VEC], o2[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      y1[e] = narrow<T, M>(mul_rn(widen<T, M>(w1[e]), rnd<T, M>(mul_rn(widen<T, M>(x1[r][e]), rs))));
+      y2[e] = narrow<T, M>(mul_rn(widen<T, M>(w2[e]), rnd<T, M>(mul_rn(widen<T, M>(x2[r][e]), rs))));
+      cs[e] = tab_c[r][j + e];
+      sn[e] = tab_s[r][j + e];
+    }
+    rotate_pair<T, M, VEC>(y1, y2, cs, cs, sn, sn, o1, o2);
+    T* orow = out + (row0 + r) * os;
+    store_vec_stream<T, VEC>(orow + c1, o1);
+    store_vec_stream<T, VEC>(orow + c2, o2);
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // SiLU-gate: out = silu(gate) * up with silu(g) = g / (1 + exp(-g)) rounded to T first.
 // ---------------------------------------------------------------------------------------
@@ -313,22 +430,22 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ g, 
                                                        const T* __restrict__ u, int64_t us,
                                                        T* __restrict__ out, int64_t os,
                                                        int64_t N, int I) {
+  // grid: x over VEC-wide chunks of a row, y over rows (strided when N exceeds the grid)
   typedef typename math_of<T>::type M;
-  const int nch = I / VEC;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= N * nch) return;
-  const int64_t row = t / nch;
-  const int c = (int)(t % nch) * VEC;
-  T gv[VEC], uv[VEC], ov[VEC];
-  load_vec<T, VEC>(g + row * gs + c, gv);
-  load_vec<T, VEC>(u + row * us + c, uv);
+  const int c = (int)(blockIdx.x * 256 + threadIdx.x) * VEC;
+  if (c >= I) return;
+  for (int64_t row = blockIdx.y; row < N; row += gridDim.y) {
+    T gv[VEC], uv[VEC], ov[VEC];
+    load_vec<T, VEC>(g + row * gs + c, gv);
+    load_vec<T, VEC>(u + row * us + c, uv);
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    const M a = widen<T, M>(gv[e]);
-    const M sl = rnd<T, M>(div_rn(a, add_rn((M)1, exp_acc(-a))));
-    ov[e] = narrow<T, M>(mul_rn(sl, widen<T, M>(uv[e])));
+    for (int e = 0; e < VEC; ++e) {
+      const M a = widen<T, M>(gv[e]);
+      const M sl = rnd<T, M>(div_rn(a, add_rn((M)1, exp_acc(-a))));
+      ov[e] = narrow<T, M>(mul_rn(sl, widen<T, M>(uv[e])));
+    }
+    store_vec_stream<T, VEC>(out + row * os + c, ov);
   }
-  store_vec<T, VEC>(out + row * os + c, ov);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -447,6 +564,10 @@ int launch_apply_rotary(const cea_tensor* x, const cea_tensor* c, const cea_tens
   return CEA_EUNSUPPORTED;
 }
 
+#ifndef CEA_RR_ROWS
+#define CEA_RR_ROWS 2  // rows per block of the single-pass RMSNorm + rotary kernel
+#endif
+
 template <typename T>
 static int rmsnorm_rope_typed(const cea_tensor* x, const cea_tensor* w, double eps,
                               const cea_tensor* pos, const cea_tensor* inv, int H,
@@ -462,7 +583,13 @@ static int rmsnorm_rope_typed(const cea_tensor* x, const cea_tensor* w, double e
 #define CEA_RR_ARGS                                                                    \
   (const T*)x->data, x->stride[0], (const T*)w->data, (const int64_t*)pos->data, ps,   \
       (const typename math_of<T>::type*)inv->data, (T*)o->data, o->stride[0], H, D, eps
-  if (vec)
+  if (vec && H * (half / V) <= 256 && half <= 256) {
+    constexpr int R = CEA_RR_ROWS;
+    hipLaunchKernelGGL((rmsnorm_rope_rows_kernel<T, V, R>), dim3((unsigned)((S + R - 1) / R)),
+                       dim3(256), 0, st, (const T*)x->data, x->stride[0], (const T*)w->data,
+                       (const int64_t*)pos->data, ps, (const typename math_of<T>::type*)inv->data,
+                       (T*)o->data, o->stride[0], S, H, D, eps);
+  } else if (vec)
     hipLaunchKernelGGL((rmsnorm_rope_kernel<T, V>), dim3(S), dim3(256), 0, st, CEA_RR_ARGS);
   else
     hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 1>), dim3(S), dim3(256), 0, st, CEA_RR_ARGS);
@@ -493,15 +620,14 @@ static int silu_mul_typed(const cea_tensor* g, const cea_tensor* u, cea_tensor* 
   const bool vec = I % V == 0 && al(g->data, 16) && al(u->data, 16) && al(o->data, 16) &&
                    strides_ok({g->stride[0], u->stride[0], o->stride[0]}, sizeof(T), 16);
   const int vw = vec ? V : 1;
-  const int64_t total = N * (I / vw);
-  if (total == 0) return CEA_OK;
-  const int64_t blocks = (total + 255) / 256;
+  if (N == 0 || I / vw == 0) return CEA_OK;
+  const dim3 grid((unsigned)((I / vw + 255) / 256), (unsigned)(N < 65535 ? N : 65535));
   if (vec)
-    hipLaunchKernelGGL((silu_mul_kernel<T, V>), dim3(blocks), dim3(256), 0, st,
+    hipLaunchKernelGGL((silu_mul_kernel<T, V>), grid, dim3(256), 0, st,
                        (const T*)g->data, g->stride[0], (const T*)u->data, u->stride[0],
                        (T*)o->data, o->stride[0], N, I);
   else
-    hipLaunchKernelGGL((silu_mul_kernel<T, 1>), dim3(blocks), dim3(256), 0, st,
+    hipLaunchKernelGGL((silu_mul_kernel<T, 1>), grid, dim3(256), 0, st,
                        (const T*)g->data, g->stride[0], (const T*)u->data, u->stride[0],
                        (T*)o->data, o->stride[0], N, I);
   CEA_CHECK_LAUNCH("silu_mul");

@@ -2,11 +2,11 @@
 SiLU gate) against the CPU oracle, through the C ABI.
 
 Tolerances (written here, used below):
-* bf16: every element within one bf16 ulp of the oracle (the oracle rounds at the
+* bf16 and f16: every element within one ulp of its dtype of the oracle (the oracle rounds at the
   reference's points, so only a last-bit difference of a transcendental or an f32
   intermediate can remain), at most 1e-3 of the elements differing at all, and
   max |diff| <= 2e-2 over elements with |ref| < 2 (the workload's absolute bound; above 2 a
-  single ulp is larger than 2e-2, and the ulp bound applies).  For RMSNorm followed by
+  single bf16 ulp is larger than 2e-2, and the ulp bound applies).  For RMSNorm followed by
   rotary, a last-bit flip of the normalised value y propagates through x*cos + rot*sin,
   whose sum may be much smaller than its terms: there the bound is two ulps of the larger
   term magnitude max(|y_i|, |y_j|) of the rotated pair, with the same 1e-3 and 2e-2 rules
@@ -26,9 +26,11 @@ from oracle import layers_ref as L
 pytestmark = pytest.mark.gpu
 
 
-def _ulp_bf16(x: torch.Tensor) -> torch.Tensor:
-    e = torch.floor(torch.log2(x.abs().clamp(min=2.0 ** -126)))
-    return torch.exp2(e - 7)
+def _ulp(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Spacing of ``dtype`` (bf16 or f16) at magnitude |x|."""
+    mant, emin = (7, -126) if dtype == torch.bfloat16 else (10, -14)
+    e = torch.floor(torch.log2(x.abs().clamp(min=2.0 ** emin)))
+    return torch.exp2(e - mant)
 
 
 def assert_close_layer(y: torch.Tensor, ref: torch.Tensor, what: str, mag: torch.Tensor = None,
@@ -48,8 +50,8 @@ def assert_close_layer(y: torch.Tensor, ref: torch.Tensor, what: str, mag: torch
     m = b.abs() if mag is None else mag.float().abs()
     diff = (a - b).abs()
     assert torch.isfinite(a).all(), f"{what}: non-finite values"
-    over = diff > _ulp_bf16(m) * ulps * 1.0001
-    assert not over.any(), f"{what}: {int(over.sum())} elements beyond {ulps} bf16 ulp, max {diff.max().item():.3e}"
+    over = diff > _ulp(m, y.dtype) * ulps * 1.0001
+    assert not over.any(), f"{what}: {int(over.sum())} elements beyond {ulps} ulp, max {diff.max().item():.3e}"
     frac = (diff > 0).float().mean().item()
     assert frac <= 1e-3, f"{what}: {frac:.2e} of the elements differ"
     small = m < 2
@@ -86,7 +88,7 @@ def test_rmsnorm_module_mixed_dtypes_and_views(cea, dev):
                        "rmsnorm view")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.float64])
 def test_rope_tables_and_rotary(cea, dev, dtype):
     S, H, D = 4096, 32, 128
     pos = torch.arange(S).view(1, S)
@@ -119,7 +121,7 @@ def test_rotary_embedding_module_llama3_scaling(cea, dev):
     assert (sin.cpu() - rs).abs().max().item() <= 2e-6
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_rmsnorm_rope_fused(cea, dev, dtype):
     """RMSNorm [4096, 4096] then rotary on the [1, 4096, 32, 128] view at positions 0..4095."""
     S, H, D = 4096, 32, 128
@@ -135,8 +137,35 @@ def test_rmsnorm_rope_fused(cea, dev, dtype):
                        mag=pair, ulps=2.0)
 
 
+@pytest.mark.parametrize("S,H,D,dtype", [
+    (7, 3, 64, torch.bfloat16),      # odd row count, 12 of 256 threads own a chunk
+    (5, 8, 512, torch.float16),      # D/2 = 256: the largest single-pass table
+    (3, 2, 1024, torch.bfloat16),    # D/2 = 512: the two-pass kernel
+    (9, 64, 128, torch.bfloat16),    # 512 chunks per row: the two-pass kernel
+    (6, 4, 96, torch.float32),       # 4-wide f32 chunks
+])
+def test_rmsnorm_rope_shapes(cea, dev, S, H, D, dtype):
+    """Row counts that leave a partial block, rows with idle threads, both kernels, a
+    row-strided input view and negative (clamped) positions."""
+    base = torch.randn(S, H * D + 64, generator=_gen(11)).to(dtype)
+    x = base[:, :H * D]  # row stride H*D + 64
+    w = (1 + 0.05 * torch.randn(H * D, generator=_gen(12))).to(dtype)
+    pos = torch.randint(-3, 5000, (S,), generator=_gen(13))
+    inv = L.inv_freq(D, 1e4)
+    y = cea.rmsnorm_rope(base.to(dev)[:, :H * D], w.to(dev), 1e-6, pos.to(dev), inv.to(dev), H)
+    torch.cuda.synchronize()
+    normed = L.rmsnorm(x, w, 1e-6).view(1, S, H, D).float()
+    pair = torch.maximum(normed.abs(), L.rotate_half(normed).abs())
+    ref = L.rmsnorm_rope(x, w, 1e-6, pos, inv, H)
+    if dtype == torch.float32:
+        assert (y.cpu() - ref).abs().max().item() <= 1e-5 * max(1.0, ref.abs().max().item())
+    else:
+        assert_close_layer(y, ref, f"rmsnorm_rope {S}x{H}x{D} {dtype}", mag=pair, ulps=2.0)
+
+
 @pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (4096, 14336)), (torch.float32, (100, 3000)),
-                                         (torch.float64, (10, 77))])
+                                         (torch.float64, (10, 77)), (torch.bfloat16, (70000, 24)),
+                                         (torch.float16, (3, 2056))])
 def test_silu_mul(cea, dev, dtype, shape):
     g = torch.randn(*shape, generator=_gen(8)).to(dtype)
     u = torch.randn(*shape, generator=_gen(9)).to(dtype)
