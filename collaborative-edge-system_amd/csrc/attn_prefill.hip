@@ -215,20 +215,24 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
                     (16 * (grp & 1) + 4 * (src & 3)) * 2;
   }
 
+  // LDS byte address of the dynamic LDS block and of this wave's 1 KB load windows in a
+  // stage (wave-uniform: scalar registers)
+  const uint32_t smem_lds = lds_addr(smem);
+  const uint32_t wave_kv = __builtin_amdgcn_readfirstlane(wave) * (L::KV_LOADS * 1024);
+  const uint32_t wave_pos = __builtin_amdgcn_readfirstlane(wave) * 64;
   auto load_tile = [&](int t, int stage) {
     const int key0 = t * BN;
     const int left = p.Sk - key0;  // > 0 for every listed tile
     const auto krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, (uint32_t)(left - 1) * krow_bytes + L::KROW);
     const auto vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, (uint32_t)(left - 1) * vrow_bytes + L::KROW);
-    char* st = smem + stage * L::STAGE_BYTES;
+    const uint32_t st = smem_lds + stage * L::STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < L::KV_LOADS; ++i) buffer_load_lds16_m0(krs, st + wave_kv + i * 1024, k_voff[i]);
 #pragma unroll
     for (int i = 0; i < L::KV_LOADS; ++i)
-      buffer_load_lds16(krs, st + (wave * L::KV_LOADS + i) * 1024, k_voff[i]);
-#pragma unroll
-    for (int i = 0; i < L::KV_LOADS; ++i)
-      buffer_load_lds16(vrs, st + L::K_BYTES + (wave * L::KV_LOADS + i) * 1024, v_voff[i]);
+      buffer_load_lds16_m0(vrs, st + L::K_BYTES + wave_kv + i * 1024, v_voff[i]);
     const auto prs = make_rsrc(pbase + (int64_t)key0 * 8, (uint32_t)left * 8);
-    if (lane < 16) buffer_load_lds4(prs, st + L::K_BYTES + L::V_BYTES + wave * 64, p_voff);
+    if (lane < 16) buffer_load_lds4_m0(prs, st + L::K_BYTES + L::V_BYTES + wave_pos, p_voff);
   };
 
   f32x16 oacc[D / 32];
@@ -245,9 +249,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   typedef const __attribute__((address_space(4))) TileInfo* tinfo_const_ptr;
   const tinfo_const_ptr tinfo_c = (tinfo_const_ptr)tinfo;
 
-  auto compute = [&](int stage, int t) {
-    const int n_valid = tinfo_c[t].n_valid;
-    const int64_t min_valid = tinfo_c[t].min_valid, max_valid = tinfo_c[t].max_valid;
+  // the summary of a tile is loaded (scalar loads) one step before the step that uses it
+  struct Summary {
+    int n_valid;
+    int64_t min_valid, max_valid;
+  };
+  auto summary = [&](int t) {
+    Summary u;
+    u.n_valid = tinfo_c[t].n_valid;
+    u.min_valid = tinfo_c[t].min_valid;
+    u.max_valid = tinfo_c[t].max_valid;
+    return u;
+  };
+  auto compute = [&](int stage, int t, const Summary& u) {
+    const int n_valid = u.n_valid;
+    const int64_t min_valid = u.min_valid, max_valid = u.max_valid;
     int mode;  // 0 skip, 1 full, 2 element-masked
     if (!wave_active || n_valid == 0 || (p.causal && qmax_w < min_valid)) mode = 0;
     else if (n_valid == BN && (!p.causal || max_valid <= qmin_w)) mode = 1;
@@ -388,15 +404,27 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     }
     if (n == 0) continue;
     int issued = 0;
-    for (; issued < n && issued < NSTAGE - 1; ++issued) load_tile(tile_list[issued], issued % NSTAGE);
+    for (; issued < n && issued < NSTAGE - 1; ++issued)
+      load_tile(__builtin_amdgcn_readfirstlane(tile_list[issued]), issued % NSTAGE);
+    // list entries of the next step (the tile to compute and the tile to load) and the
+    // summary of the tile to compute are fetched at the end of the previous step, so the
+    // step itself waits for neither LDS nor scalar-load latency
+    int t_cur = __builtin_amdgcn_readfirstlane(tile_list[0]);
+    int t_load = issued < n ? __builtin_amdgcn_readfirstlane(tile_list[issued]) : 0;
+    Summary u_cur = summary(t_cur);
     for (int i = 0; i < n; ++i) {
       wait_tiles_ahead<L::LOADS_PER_TILE>(issued - i - 1);
       barrier_no_fence();  // tile i landed for every wave; the stage of tile i-1 is free
       if (issued < n) {
-        load_tile(tile_list[issued], issued % NSTAGE);
+        load_tile(t_load, issued % NSTAGE);
         ++issued;
       }
-      compute(i % NSTAGE, __builtin_amdgcn_readfirstlane(tile_list[i]));
+      compute(i % NSTAGE, t_cur, u_cur);
+      if (i + 1 < n) {
+        t_cur = __builtin_amdgcn_readfirstlane(tile_list[i + 1]);
+        if (issued < n) t_load = __builtin_amdgcn_readfirstlane(tile_list[issued]);
+        u_cur = summary(t_cur);
+      }
     }
     __syncthreads();  // the next pass rewrites the list and the stages
   }
