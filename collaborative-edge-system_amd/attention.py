@@ -205,13 +205,16 @@ def attention_with_lse_into(
     causal: bool = True,
     scale: Optional[float] = None,
     kv_map: KVMap = None,
+    accumulate: bool = True,
 ) -> None:
     """Merges attention over one more KV block into a running ``(out, lse)`` in place.
 
     Equivalent to ``out, lse = merge_attention(out, lse, *attention_with_lse(...))`` (the
     online merge of ring attention, sequence_parallel.py:117-121) without materialising the
     block's partial result: the merge runs in the attention kernel's epilogue.  Start from
-    ``out = 0``, ``lse = -inf`` (the merge's neutral element).
+    ``out = 0``, ``lse = -inf`` (the merge's neutral element), or pass
+    ``accumulate=False`` for the first block: its result then overwrites ``(out, lse)``,
+    which need no initialisation (an empty block leaves them untouched either way).
     """
     if k.shape[1] == 0 or q.shape[1] == 0:
         return
@@ -220,7 +223,7 @@ def attention_with_lse_into(
     acc = accumulation_dtype(q.dtype)
     if out.dtype != acc or lse.dtype != acc:
         raise ValueError(f"running (out, lse) must be {acc}")
-    _launch(q, k, v, q_pos, k_pos, causal, scale, mapping, out, lse, True)
+    _launch(q, k, v, q_pos, k_pos, causal, scale, mapping, out, lse, bool(accumulate))
 
 
 def merge_attention(

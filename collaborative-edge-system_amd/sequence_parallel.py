@@ -138,9 +138,11 @@ def ring_attention_with_lse(
         raise ValueError(f"kv_sizes {list(kv_sizes)} inconsistent with local block of {k.shape[1]} tokens")
     B, Sq, Hq, D = q.shape
     acc = accumulation_dtype(q.dtype)
-    out = torch.zeros(B, Sq, Hq, D, dtype=acc, device=q.device)
-    lse = torch.full((B, Hq, Sq), float("-inf"), dtype=acc, device=q.device)
+    # the first non-empty block writes (out, lse); later ones merge into them in the kernel
+    out = torch.empty(B, Sq, Hq, D, dtype=acc, device=q.device)
+    lse = torch.empty((B, Hq, Sq), dtype=acc, device=q.device)
     own = (k, v, k_pos)
+    first = True
     for step in range(n):
         kb, vb, pb = _kv_from(comm, (r - step) % n, own)
         if kb.shape[1] != kv_sizes[(r - step) % n]:
@@ -149,7 +151,12 @@ def ring_attention_with_lse(
         for start in range(0, kb.shape[1], max(1, blk)):
             end = min(start + blk, kb.shape[1])
             attention_with_lse_into(out, lse, q, kb[:, start:end], vb[:, start:end], q_pos,
-                                    pb[:, start:end], causal=causal, scale=scale, kv_map=kv_map)
+                                    pb[:, start:end], causal=causal, scale=scale, kv_map=kv_map,
+                                    accumulate=not first)
+            first = False
+    if first:  # no rank held a key: the merge's neutral element
+        out.zero_()
+        lse.fill_(float("-inf"))
     return out, lse
 
 
