@@ -161,6 +161,17 @@ def bench_layers(cea, torch, steps, warmup, dev):
     return res
 
 
+def bench_kv_append(cea, torch, steps, warmup, dev):
+    w = cea.workloads.kv_append(device=dev)
+    sec = _graph_timed(lambda: cea.kv_append(w.cache_k, w.cache_v, w.cache_pos, w.offset, w.k, w.v,
+                                             w.pos, w.cos, w.sin), steps, warmup, torch)
+    gbs = w.bytes / sec / 1e9
+    return {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "us_per_step": round(sec * 1e6, 2), "bytes": w.bytes,
+            "workload": "rotary-K + head-major KV-cache append: 8192 tokens x 8 KV heads x 128, "
+                        "bf16, into a cache holding 8192 tokens; timed as HIP-graph replays"}
+
+
 def bench_ulysses(cea, torch, steps, warmup, dev):
     w = cea.workloads.ulysses_share(device=dev)
 
@@ -227,7 +238,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,ulysses,f32")
+    ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,kvappend,ulysses,f32")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a device copy of MIB MiB (HBM counter calibration) and exit")
@@ -264,6 +275,9 @@ def main() -> int:
     if want("layers"):
         _log("layer ops")
         secondary["layer_ops"] = bench_layers(cea, torch, args.steps, args.warmup, dev)
+    if want("kvappend"):
+        _log("kv-cache append")
+        secondary["kv_append"] = bench_kv_append(cea, torch, args.steps, args.warmup, dev)
     if want("ulysses"):
         _log("ulysses share")
         secondary["ulysses_share"] = bench_ulysses(cea, torch, max(3, args.steps // 4), 1, dev)

@@ -7,11 +7,13 @@ Import with ``importlib.import_module("collaborative-edge-system_amd")``.  Modul
 * :mod:`.sequence_parallel` - one rank's ring / Ulysses / distributed-KV share on one GPU
   (collab_infer/parallel/sequence_parallel.py)
 * :mod:`.layers` - RMSNorm, rotary, SiLU-gate (collab_infer/models/llama.py)
+* :mod:`.kv_cache` - head-major KV cache with the rotary of K fused into the append
+  (collab_infer/models/cache.py)
 * :mod:`.partition` - splits and sequence layouts (collab_infer/parallel/partition.py)
 * :mod:`.workloads` - seeded inputs of the five measured workloads
 """
 
-from . import _native, attention, layers, partition, sequence_parallel, workloads  # noqa: F401
+from . import _native, attention, kv_cache, layers, partition, sequence_parallel, workloads  # noqa: F401
 from .attention import (  # noqa: F401
     MASK_CHUNK_ELEMENTS,
     accumulation_dtype,
@@ -25,6 +27,7 @@ from .attention import (  # noqa: F401
     merge_attention_list,
     visibility_mask,
 )
+from .kv_cache import LayerKVCache, kv_append  # noqa: F401
 from .layers import RMSNorm, RotaryEmbedding, apply_rotary, rmsnorm, rmsnorm_rope, silu_mul  # noqa: F401
 from .partition import HeadShard, SequenceLayout, partition_heads, split_sizes  # noqa: F401
 from .sequence_parallel import (  # noqa: F401

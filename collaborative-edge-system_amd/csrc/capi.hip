@@ -513,6 +513,52 @@ int cea_apply_rotary(const cea_tensor* x, const cea_tensor* cos, const cea_tenso
   return launch_apply_rotary(x, &c, &s, out, (hipStream_t)stream);
 }
 
+int cea_kv_append(const cea_tensor* k, const cea_tensor* v, const cea_tensor* pos,
+                  const cea_tensor* cos, const cea_tensor* sin, cea_tensor* cache_k,
+                  cea_tensor* cache_v, cea_tensor* cache_pos, int64_t offset, void* stream) {
+  int rc;
+  if ((rc = check_tensor(k, "k", 4, -1, true))) return rc;
+  const int dt = k->dtype;
+  if ((rc = check_tensor(v, "v", 4, dt, true))) return rc;
+  if ((rc = check_tensor(pos, "positions", 2, CEA_I64, false))) return rc;
+  if ((rc = check_tensor(cache_k, "cache_k", 4, dt, true))) return rc;
+  if ((rc = check_tensor(cache_v, "cache_v", 4, dt, true))) return rc;
+  if ((rc = check_tensor(cache_pos, "cache_pos", 2, CEA_I64, false))) return rc;
+  const int64_t B = k->size[0], n = k->size[1], H = k->size[2], D = k->size[3];
+  for (int i = 0; i < 4; ++i)
+    CEA_REQUIRE(v->size[i] == k->size[i], CEA_EINVAL, "kv_append: v must match k [B,n,H,D]");
+  CEA_REQUIRE(pos->size[0] == B && pos->size[1] == n, CEA_EINVAL,
+              "kv_append: positions must be [B, n]");
+  const int64_t cap = cache_k->size[2];
+  for (const cea_tensor* c : {(const cea_tensor*)cache_k, (const cea_tensor*)cache_v})
+    CEA_REQUIRE(c->size[0] == B && c->size[1] == H && c->size[2] == cap && c->size[3] == D,
+                CEA_EINVAL, "kv_append: caches must be [B, H, capacity, D]");
+  CEA_REQUIRE(cache_pos->size[0] == B && cache_pos->size[1] == cap, CEA_EINVAL,
+              "kv_append: cache positions must be [B, capacity]");
+  CEA_REQUIRE(offset >= 0 && offset + n <= cap, CEA_EINVAL,
+              "kv_append: slots %lld..%lld exceed the capacity %lld", (long long)offset,
+              (long long)(offset + n), (long long)cap);
+  CEA_REQUIRE((cos == nullptr) == (sin == nullptr), CEA_EINVAL,
+              "kv_append: give both rotary tables or neither");
+  cea_tensor c, sn;
+  if (cos) {
+    if ((rc = check_tensor(cos, "cos", 3, dt, true))) return rc;
+    if ((rc = check_tensor(sin, "sin", 3, dt, true))) return rc;
+    CEA_REQUIRE(D % 2 == 0, CEA_EINVAL, "kv_append: head size must be even to rotate");
+    for (const cea_tensor* t : {cos, sin})
+      CEA_REQUIRE((t->size[0] == B || t->size[0] == 1) && t->size[1] == n && t->size[2] == D,
+                  CEA_EINVAL, "kv_append: cos/sin must be [B, n, D]");
+    c = *cos;
+    sn = *sin;
+    if (c.size[0] == 1) c.stride[0] = 0;  // broadcast over the batch
+    if (sn.size[0] == 1) sn.stride[0] = 0;
+  } else {
+    CEA_REQUIRE(D % 2 == 0, CEA_EINVAL, "kv_append: head size must be even");
+  }
+  return launch_kv_append(k, v, pos, cos ? &c : nullptr, cos ? &sn : nullptr, cache_k, cache_v,
+                          cache_pos, offset, (hipStream_t)stream);
+}
+
 int cea_rmsnorm_rope(const cea_tensor* x, const cea_tensor* weight, double eps,
                      const cea_tensor* positions, const cea_tensor* inv_freq, int32_t num_heads,
                      cea_tensor* out, void* stream) {

@@ -98,6 +98,9 @@ int launch_rope_tables(const cea_tensor* pos, const cea_tensor* inv, cea_tensor*
                        cea_tensor* sn, hipStream_t s);
 int launch_apply_rotary(const cea_tensor* x, const cea_tensor* c, const cea_tensor* sn,
                         cea_tensor* o, hipStream_t s);
+int launch_kv_append(const cea_tensor* k, const cea_tensor* v, const cea_tensor* pos,
+                     const cea_tensor* c, const cea_tensor* sn, cea_tensor* ck, cea_tensor* cv,
+                     cea_tensor* cp, int64_t offset, hipStream_t st);
 int launch_rmsnorm_rope(const cea_tensor* x, const cea_tensor* w, double eps,
                         const cea_tensor* pos, const cea_tensor* inv, int H, cea_tensor* o,
                         hipStream_t s);

@@ -258,6 +258,64 @@ __global__ __launch_bounds__(256) void apply_rotary_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
+// KV-cache append: token-major k, v [B,n,H,D] (k optionally rotated first, exactly as
+// apply_rotary) written into head-major caches [B,H,cap,D] at slots offset..offset+n, and
+// the positions into [B,cap].  One thread owns VEC features of the first half and the
+// matching VEC of the second half of one (b, token, head) row, for k and for v.
+// ---------------------------------------------------------------------------------------
+template <typename T, int VEC, bool ROT>
+__global__ __launch_bounds__(256) void kv_append_kernel(
+    const T* __restrict__ k, int64_t ks_b, int64_t ks_s, int64_t ks_h,
+    const T* __restrict__ v, int64_t vs_b, int64_t vs_s, int64_t vs_h,
+    const T* __restrict__ cosb, int64_t cs_b, int64_t cs_s, const T* __restrict__ sinb,
+    int64_t ss_b, int64_t ss_s, const int64_t* __restrict__ pos, int64_t ps_b, int64_t ps_s,
+    T* __restrict__ ck, int64_t cks_b, int64_t cks_h, int64_t cks_s,
+    T* __restrict__ cv, int64_t cvs_b, int64_t cvs_h, int64_t cvs_s,
+    int64_t* __restrict__ cpos, int64_t cps_b, int64_t cps_s, int64_t offset, int B, int n,
+    int H, int D) {
+  typedef typename math_of<T>::type M;
+  const int half = D / 2;
+  const int nch = half / VEC;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)B * n * H * nch;
+  if (t >= total) return;
+  const int j = (int)(t % nch) * VEC;
+  int64_t r = t / nch;
+  const int h = (int)(r % H);
+  r /= H;
+  const int s = (int)(r % n);
+  const int b = (int)(r / n);
+  const int64_t slot = offset + s;
+  const T* kr = k + b * ks_b + s * ks_s + h * ks_h;
+  const T* vr = v + b * vs_b + s * vs_s + h * vs_h;
+  T* ckr = ck + b * cks_b + h * cks_h + slot * cks_s;
+  T* cvr = cv + b * cvs_b + h * cvs_h + slot * cvs_s;
+  T k1[VEC], k2[VEC], v1[VEC], v2[VEC];
+  load_vec<T, VEC>(kr + j, k1);
+  load_vec<T, VEC>(kr + j + half, k2);
+  load_vec<T, VEC>(vr + j, v1);
+  load_vec<T, VEC>(vr + j + half, v2);
+  if constexpr (ROT) {
+    const T* cr = cosb + b * cs_b + s * cs_s;
+    const T* sr = sinb + b * ss_b + s * ss_s;
+    T c1[VEC], c2[VEC], s1[VEC], s2[VEC], o1[VEC], o2[VEC];
+    load_vec<T, VEC>(cr + j, c1);
+    load_vec<T, VEC>(cr + j + half, c2);
+    load_vec<T, VEC>(sr + j, s1);
+    load_vec<T, VEC>(sr + j + half, s2);
+    rotate_pair<T, M, VEC>(k1, k2, c1, c2, s1, s2, o1, o2);
+    store_vec<T, VEC>(ckr + j, o1);
+    store_vec<T, VEC>(ckr + j + half, o2);
+  } else {
+    store_vec<T, VEC>(ckr + j, k1);
+    store_vec<T, VEC>(ckr + j + half, k2);
+  }
+  store_vec<T, VEC>(cvr + j, v1);
+  store_vec<T, VEC>(cvr + j + half, v2);
+  if (h == 0 && j == 0) cpos[b * cps_b + slot * cps_s] = pos[b * ps_b + s * ps_s];
+}
+
+// ---------------------------------------------------------------------------------------
 // fused RMSNorm + rotary: one 256-thread block per token row of H*D features.  The row's
 // rotary tables (D/2 angles) are evaluated once into LDS; every feature pair (j, j+D/2) of
 // every head is normalised, weighted and rotated in registers.
@@ -561,6 +619,63 @@ int launch_apply_rotary(const cea_tensor* x, const cea_tensor* c, const cea_tens
     case CEA_F64: return apply_rotary_typed<double>(x, c, s, o, st);
   }
   set_error("apply_rotary: unsupported dtype %s", dtype_name(x->dtype));
+  return CEA_EUNSUPPORTED;
+}
+
+template <typename T>
+static int kv_append_typed(const cea_tensor* k, const cea_tensor* v, const cea_tensor* pos,
+                           const cea_tensor* c, const cea_tensor* sn, cea_tensor* ck,
+                           cea_tensor* cv, cea_tensor* cp, int64_t offset, hipStream_t st) {
+  const int B = (int)k->size[0], n = (int)k->size[1], H = (int)k->size[2], D = (int)k->size[3];
+  const int half = D / 2;
+  const bool rot = c != nullptr;
+  constexpr int V = 16 / sizeof(T);
+  bool vec = half % V == 0 && al(k->data, 16) && al(v->data, 16) && al(ck->data, 16) &&
+             al(cv->data, 16) &&
+             strides_ok({k->stride[0], k->stride[1], k->stride[2], v->stride[0], v->stride[1],
+                         v->stride[2], ck->stride[0], ck->stride[1], ck->stride[2],
+                         cv->stride[0], cv->stride[1], cv->stride[2], (int64_t)half},
+                        sizeof(T), 16);
+  if (rot)
+    vec = vec && al(c->data, 16) && al(sn->data, 16) &&
+          strides_ok({c->stride[0], c->stride[1], sn->stride[0], sn->stride[1]}, sizeof(T), 16);
+  const int vecw = vec ? V : 1;
+  const int64_t total = (int64_t)B * n * H * (half / vecw);
+  if (total == 0) return CEA_OK;
+  const int64_t blocks = (total + 255) / 256;
+  const T* cd = rot ? (const T*)c->data : nullptr;
+  const T* sd = rot ? (const T*)sn->data : nullptr;
+  const int64_t c0 = rot ? c->stride[0] : 0, c1 = rot ? c->stride[1] : 0;
+  const int64_t s0 = rot ? sn->stride[0] : 0, s1 = rot ? sn->stride[1] : 0;
+#define CEA_KV_ARGS                                                                          \
+  (const T*)k->data, k->stride[0], k->stride[1], k->stride[2], (const T*)v->data,             \
+      v->stride[0], v->stride[1], v->stride[2], cd, c0, c1, sd, s0, s1,                      \
+      (const int64_t*)pos->data, pos->stride[0], pos->stride[1], (T*)ck->data, ck->stride[0], \
+      ck->stride[1], ck->stride[2], (T*)cv->data, cv->stride[0], cv->stride[1],              \
+      cv->stride[2], (int64_t*)cp->data, cp->stride[0], cp->stride[1], offset, B, n, H, D
+  if (vec && rot)
+    hipLaunchKernelGGL((kv_append_kernel<T, V, true>), dim3(blocks), dim3(256), 0, st, CEA_KV_ARGS);
+  else if (vec)
+    hipLaunchKernelGGL((kv_append_kernel<T, V, false>), dim3(blocks), dim3(256), 0, st, CEA_KV_ARGS);
+  else if (rot)
+    hipLaunchKernelGGL((kv_append_kernel<T, 1, true>), dim3(blocks), dim3(256), 0, st, CEA_KV_ARGS);
+  else
+    hipLaunchKernelGGL((kv_append_kernel<T, 1, false>), dim3(blocks), dim3(256), 0, st, CEA_KV_ARGS);
+#undef CEA_KV_ARGS
+  CEA_CHECK_LAUNCH("kv_append");
+  return CEA_OK;
+}
+
+int launch_kv_append(const cea_tensor* k, const cea_tensor* v, const cea_tensor* pos,
+                     const cea_tensor* c, const cea_tensor* sn, cea_tensor* ck, cea_tensor* cv,
+                     cea_tensor* cp, int64_t offset, hipStream_t st) {
+  switch (k->dtype) {
+    case CEA_BF16: return kv_append_typed<bf16>(k, v, pos, c, sn, ck, cv, cp, offset, st);
+    case CEA_F16: return kv_append_typed<f16>(k, v, pos, c, sn, ck, cv, cp, offset, st);
+    case CEA_F32: return kv_append_typed<float>(k, v, pos, c, sn, ck, cv, cp, offset, st);
+    case CEA_F64: return kv_append_typed<double>(k, v, pos, c, sn, ck, cv, cp, offset, st);
+  }
+  set_error("kv_append: unsupported dtype %s", dtype_name(k->dtype));
   return CEA_EUNSUPPORTED;
 }
 

@@ -17,6 +17,8 @@ CPU oracle and the GPU see bit-identical inputs.
   uniform in [1024, 32768]; four contiguous partitions with weights 0.4/0.3/0.2/0.1.
 * ``ulysses_share``    - rank 0 of an 8-way Ulysses split of a 64/16-head model: 65536 tokens,
   8/2 heads, D=128, bf16, causal, 4 packed sequences followed by right padding.
+* ``kv_append``        - one rank's 8192-token prefill chunk (8 KV heads, D=128, bf16, theta
+  1e4) rotated and appended into a head-major cache that already holds 8192 tokens.
 """
 
 from __future__ import annotations
@@ -257,3 +259,42 @@ __all__ = [
     "ulysses_share",
     "visible_pairs",
 ]
+
+
+@dataclass
+class KVAppend:
+    k: torch.Tensor          # [1, n, Hkv, D] token-major, before the rotary
+    v: torch.Tensor
+    pos: torch.Tensor        # [1, n]
+    cos: torch.Tensor        # [1, n, D]
+    sin: torch.Tensor
+    cache_k: torch.Tensor    # [1, Hkv, capacity, D]
+    cache_v: torch.Tensor
+    cache_pos: torch.Tensor  # [1, capacity]
+    offset: int
+
+    @property
+    def bytes(self) -> int:
+        # k, v read and written once, the tables read once (shared by the heads),
+        # positions read and written
+        kv = self.k.numel() * self.k.element_size()
+        tab = self.cos.numel() * self.cos.element_size()
+        return 4 * kv + 2 * tab + 2 * self.pos.numel() * 8
+
+
+def kv_append(device="cpu", seed: int = 0, n: int = 8192, heads: int = 8, head_dim: int = 128,
+              cached: int = 8192, theta: float = 1e4) -> KVAppend:
+    g = _gen(seed)
+    k = _randn(g, 1, n, heads, head_dim, device=device)
+    v = _randn(g, 1, n, heads, head_dim, device=device)
+    pos = torch.arange(cached, cached + n, device=device).view(1, n)
+    half = torch.arange(0, head_dim, 2, dtype=torch.int64).to(torch.float32) / head_dim
+    inv = 1.0 / (theta ** half)
+    freqs = pos.to("cpu").to(torch.float32).unsqueeze(-1) * inv
+    emb = torch.cat([freqs, freqs], dim=-1)
+    cos, sin = emb.cos().to(torch.bfloat16).to(device), emb.sin().to(torch.bfloat16).to(device)
+    cap = cached + n
+    cache_k = torch.zeros(1, heads, cap, head_dim, dtype=torch.bfloat16, device=device)
+    cache_v = torch.zeros_like(cache_k)
+    cache_pos = torch.full((1, cap), -1, dtype=torch.int64, device=device)
+    return KVAppend(k, v, pos, cos, sin, cache_k, cache_v, cache_pos, cached)

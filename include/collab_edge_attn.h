@@ -156,6 +156,21 @@ int cea_apply_rotary(const cea_tensor* x, const cea_tensor* cos, const cea_tenso
                      cea_tensor* out, void* stream);
 
 /*
+ * KV-cache append with the rotary of K fused in: writes k (rotated with cos/sin exactly as
+ * cea_apply_rotary would, when the tables are given) and v, token-major [B,n,H,D], into
+ * head-major caches [B,H,capacity,D] at slots offset..offset+n-1, and the positions [B,n]
+ * into cache_pos [B,capacity].  One launch instead of apply_rotary plus two transposing
+ * copies.  Growth (reallocation) stays with the caller.
+ * Replaces `k = apply_rotary(k, cos, sin)` (collab_infer/models/llama.py:161, 196, 205, 208)
+ * followed by LayerKVCache.append (collab_infer/models/cache.py:51-62).
+ *   k, v [B,n,H,D] (any outer strides), positions [B,n] i64, cos/sin [B,n,D] or both NULL
+ *   (plain append; D must still be even), cache_k/cache_v [B,H,cap,D], cache_pos [B,cap].
+ */
+int cea_kv_append(const cea_tensor* k, const cea_tensor* v, const cea_tensor* pos,
+                  const cea_tensor* cos, const cea_tensor* sin, cea_tensor* cache_k,
+                  cea_tensor* cache_v, cea_tensor* cache_pos, int64_t offset, void* stream);
+
+/*
  * Fused RMSNorm + rotary: the RMSNorm output of x [S, H*D] viewed as [1,S,H,D] and rotated
  * at positions [S] with tables generated in-kernel (same rounding points as
  * cea_rmsnorm followed by cea_rope_tables + cea_apply_rotary).
