@@ -126,8 +126,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   typedef Layout<D> L;
   typedef typename Mfma<T>::frag frag;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  __shared__ int tile_list[LIST_CAP];
-  __shared__ int64_t red_q[NWAVES];
+  // listed tiles: (tile index, 2-bit mode of every wave: 0 skip, 1 full, 2 element-masked)
+  __shared__ int2 tile_list[LIST_CAP];
+  __shared__ int64_t red_q[NWAVES], red_qmin[NWAVES];
+  __shared__ int red_act[NWAVES];
   __shared__ int wave_cnt[NWAVES];
 
   const int tid = threadIdx.x;
@@ -156,7 +158,11 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   const int64_t qmin_w = wave_min_i64(row_ok ? qpos : INT64_MAX);
   const int64_t qmax_w = wave_max_i64(row_ok ? qpos : INT64_MIN);
   const bool wave_active = __builtin_amdgcn_readfirstlane(qb * BM + wave * 32 < p.Sq ? 1 : 0);
-  if (lane == 0) red_q[wave] = qmax_w;
+  if (lane == 0) {
+    red_q[wave] = qmax_w;
+    red_qmin[wave] = qmin_w;
+    red_act[wave] = wave_active ? 1 : 0;
+  }
   __syncthreads();
   int64_t qmax_wg = red_q[0];
 #pragma unroll
@@ -244,32 +250,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   float m_use = 0.f;                // m_run * c, or 0 while the row has seen nothing
   float l_run = 0.f;                // this lane's partial row sum
 
-  // per-tile summaries are read through the constant address space: scalar loads, counted
-  // by lgkmcnt, so reading one does not wait for the tile loads in flight (vmcnt)
-  typedef const __attribute__((address_space(4))) TileInfo* tinfo_const_ptr;
-  const tinfo_const_ptr tinfo_c = (tinfo_const_ptr)tinfo;
-
-  // the summary of a tile is loaded (scalar loads) one step before the step that uses it
-  struct Summary {
-    int n_valid;
-    int64_t min_valid, max_valid;
-  };
-  auto summary = [&](int t) {
-    Summary u;
-    u.n_valid = tinfo_c[t].n_valid;
-    u.min_valid = tinfo_c[t].min_valid;
-    u.max_valid = tinfo_c[t].max_valid;
-    return u;
-  };
-  auto compute = [&](int stage, int t, const Summary& u) {
-    const int n_valid = u.n_valid;
-    const int64_t min_valid = u.min_valid, max_valid = u.max_valid;
-    int mode;  // 0 skip, 1 full, 2 element-masked
-    if (!wave_active || n_valid == 0 || (p.causal && qmax_w < min_valid)) mode = 0;
-    else if (n_valid == BN && (!p.causal || max_valid <= qmin_w)) mode = 1;
-    else mode = 2;
-    mode = __builtin_amdgcn_readfirstlane(mode);
-    if (mode == 0) return;
+  // mode: 1 every key of the tile visible to every row of the wave, 2 element-masked
+  auto compute = [&](int stage, int t, int mode) {
     const char* sb = smem + stage * L::STAGE_BYTES;
 
     f32x16 sacc[2];
@@ -386,9 +368,18 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     for (int r0 = 0; r0 < span; r0 += NTHREADS) {
       const int t = base + r0 + tid;
       bool need = false;
+      int modes = 0;
       if (r0 + tid < span) {
         const TileInfo ti = tinfo[t];
         need = ti.n_valid > 0 && !(p.causal && qmax_wg < ti.min_valid);
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+          int m;
+          if (!red_act[w] || ti.n_valid == 0 || (p.causal && red_q[w] < ti.min_valid)) m = 0;
+          else if (ti.n_valid == BN && (!p.causal || ti.max_valid <= red_qmin[w])) m = 1;
+          else m = 2;
+          modes |= m << (2 * w);
+        }
       }
       const uint64_t bal = __ballot(need);
       if (lane == 0) wave_cnt[wave] = __builtin_popcountll(bal);
@@ -398,20 +389,27 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
       int tot = n;
       for (int w = 0; w < NWAVES; ++w) tot += wave_cnt[w];
       if (need) tile_list[off + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0))] = t;
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0))] =
+          make_int2(t, modes);
       __syncthreads();
       n = tot;
     }
     if (n == 0) continue;
     int issued = 0;
     for (; issued < n && issued < NSTAGE - 1; ++issued)
-      load_tile(__builtin_amdgcn_readfirstlane(tile_list[issued]), issued % NSTAGE);
-    // list entries of the next step (the tile to compute and the tile to load) and the
-    // summary of the tile to compute are fetched at the end of the previous step, so the
-    // step itself waits for neither LDS nor scalar-load latency
-    int t_cur = __builtin_amdgcn_readfirstlane(tile_list[0]);
-    int t_load = issued < n ? __builtin_amdgcn_readfirstlane(tile_list[issued]) : 0;
-    Summary u_cur = summary(t_cur);
+      load_tile(__builtin_amdgcn_readfirstlane(tile_list[issued].x), issued % NSTAGE);
+    // list entries of the next step (the tile to compute with this wave's mode, and the
+    // tile to load) are fetched at the end of the previous step, so the step itself does
+    // not wait for LDS latency
+    const int mshift = 2 * wave;
+    auto entry = [&](int i, int& t, int& mode) {
+      const int2 e = tile_list[i];
+      t = __builtin_amdgcn_readfirstlane(e.x);
+      mode = __builtin_amdgcn_readfirstlane((e.y >> mshift) & 3);
+    };
+    int t_cur, m_cur;
+    entry(0, t_cur, m_cur);
+    int t_load = issued < n ? __builtin_amdgcn_readfirstlane(tile_list[issued].x) : 0;
     for (int i = 0; i < n; ++i) {
       wait_tiles_ahead<L::LOADS_PER_TILE>(issued - i - 1);
       barrier_no_fence();  // tile i landed for every wave; the stage of tile i-1 is free
@@ -419,11 +417,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
         load_tile(t_load, issued % NSTAGE);
         ++issued;
       }
-      compute(i % NSTAGE, t_cur, u_cur);
+      if (m_cur != 0) compute(i % NSTAGE, t_cur, m_cur);
       if (i + 1 < n) {
-        t_cur = __builtin_amdgcn_readfirstlane(tile_list[i + 1]);
-        if (issued < n) t_load = __builtin_amdgcn_readfirstlane(tile_list[issued]);
-        u_cur = summary(t_cur);
+        entry(i + 1, t_cur, m_cur);
+        if (issued < n) t_load = __builtin_amdgcn_readfirstlane(tile_list[issued].x);
       }
     }
     __syncthreads();  // the next pass rewrites the list and the stages
