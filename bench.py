@@ -91,22 +91,28 @@ def bench_ring(cea, torch, steps, warmup, dev):
         return cea.ring_attention(w.q, k0, v0, w.q_pos, p0, comm, w.kv_sizes)
 
     sec = _timed(step, steps, warmup, torch)
-    # per-launch durations of the attention kernel call (tile summary + prefill kernel) on
-    # the stream they are launched on, over a timed ring pass
+    # average duration of one attention call (tile summary + prefill kernel) over back-to-back
+    # ring passes, from two HIP events on the stream the kernels run on (an event pair around
+    # every launch would add its own gap and cache flush to each launch)
     stream = torch.cuda.current_stream(dev)
     out = torch.zeros(w.q.shape, dtype=torch.float32, device=dev)
     lse = torch.full((1, w.q.shape[2], w.q.shape[1]), float("-inf"), device=dev)
-    evs = []
-    for _ in range(max(3, steps // 4)):
-        for src in w.ring_order:
+
+    def ring_pass():
+        for i, src in enumerate(w.ring_order):
             k, v, p = w.blocks[src]
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            cea.attention_with_lse_into(out, lse, w.q, k, v, w.q_pos, p)
-            b.record(stream)
-            evs.append((a, b))
+            cea.attention_with_lse_into(out, lse, w.q, k, v, w.q_pos, p, accumulate=i > 0)
+
+    passes = max(3, steps // 2)
+    ring_pass()
     torch.cuda.synchronize()
-    launch_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(passes):
+        ring_pass()
+    b.record(stream)
+    torch.cuda.synchronize()
+    launch_ms = a.elapsed_time(b) / (passes * len(w.ring_order))
     flop_launch = w.flop / len(w.ring_order)
     achieved = flop_launch / (launch_ms * 1e-3) / 1e12
     tflops = w.flop / sec / 1e12
@@ -170,6 +176,62 @@ def bench_kv_append(cea, torch, steps, warmup, dev):
             "us_per_step": round(sec * 1e6, 2), "bytes": w.bytes,
             "workload": "rotary-K + head-major KV-cache append: 8192 tokens x 8 KV heads x 128, "
                         "bf16, into a cache holding 8192 tokens; timed as HIP-graph replays"}
+
+
+def bench_wire(cea, torch, steps, warmup, dev):
+    """The collectives' wire formats on one device: the two Ulysses all-to-alls of rank 0 at
+    the Ulysses workload's shape (65536 tokens, 64/16 heads over sp=8, D=128, bf16), and the
+    distributed-KV decode workload through the packed all-gather route with the in-place
+    merge of the gathered [4, 32, 1, 32, 129] f32 buffer."""
+    S, world, D = 65536, 8, 128
+    heads = cea.partition_heads(64, 16, world)
+    layout = cea.SequenceLayout(S, world, None, "contiguous")
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(1, S, 64, D, generator=g, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(1, S, 16, D, generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(1, S, 16, D, generator=g, device=dev, dtype=torch.bfloat16)
+    pos = torch.arange(S, device=dev).view(1, S)
+    grp = cea.LocalGroup(world, 0)
+    shards = [tuple(layout.shard(t, r) for t in (q, k, v, pos)) for r in range(world)]
+    for r, (a, b, c, p) in enumerate(shards):
+        grp.set_shard(r, q=a, k=b, v=c, pos=p)
+    me = heads[0]
+    width = me.q_count + 2 * me.kv_count
+    res = {}
+    sec = _graph_timed(lambda: cea.ulysses_scatter(*shards[0], grp, layout.sizes, heads), steps,
+                       warmup, torch, per_graph=10)
+    nb = 2 * S * width * D * 2 + 2 * S * 8
+    res["ulysses_scatter"] = {"value": round(nb / sec / 1e9, 1), "unit": "GB/s",
+                              "frac": round(nb / sec / 1e9 / PEAK_HBM_GBS, 4),
+                              "us_per_step": round(sec * 1e6, 2), "bytes": nb}
+    outs = [torch.randn(1, S, h.q_count, D, generator=g, device=dev, dtype=torch.bfloat16)
+            for h in heads]
+    sec = _graph_timed(lambda: cea.ulysses_gather(outs, grp, layout.sizes, heads), steps, warmup,
+                       torch, per_graph=10)
+    nb = 2 * (S // world) * 64 * D * 2
+    res["ulysses_gather"] = {"value": round(nb / sec / 1e9, 1), "unit": "GB/s",
+                             "frac": round(nb / sec / 1e9 / PEAK_HBM_GBS, 4),
+                             "us_per_step": round(sec * 1e6, 2), "bytes": nb}
+    del q, k, v, outs, shards, grp
+    w = cea.workloads.kv_decode(device=dev)
+    parts = w.partitions()
+    comm = cea.LocalGroup(len(parts), 0)
+    for r, (kk, vv, pp) in enumerate(parts):
+        comm.set_shard(r, k=kk, v=vv, pos=pp)
+    sec = _timed(lambda: cea.distributed_kv_attention(w.q, *parts[0][:2], w.q_pos, parts[0][2],
+                                                      comm, wire=True), steps, warmup, torch)
+    B, Sq, Hq, _ = w.q.shape
+    gathered = torch.randn(len(parts), B, Sq, Hq, D + 1, device=dev)
+    msec = _graph_timed(lambda: cea.merge_packed(gathered, out_dtype=torch.bfloat16), steps,
+                        warmup, torch)
+    nb = gathered.numel() * 4 + B * Sq * Hq * D * 2
+    res["kv_decode_packed"] = {"ms_per_step": round(sec * 1e3, 4),
+                               "merge_packed_us": round(msec * 1e6, 2), "merge_bytes": nb,
+                               "merge_gbs": round(nb / msec / 1e9, 1)}
+    res["workload"] = ("Ulysses sp=8 all-to-alls of rank 0 (65536 tokens, 64/16 heads, D=128, "
+                       "bf16; HIP-graph replays); distributed-KV decode via pack + gathered "
+                       "[4,32,1,32,129] f32 buffer + in-place merge to bf16")
+    return res
 
 
 def bench_ulysses(cea, torch, steps, warmup, dev):
@@ -238,7 +300,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,kvappend,ulysses,f32")
+    ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,kvappend,ulysses,wire,f32")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a device copy of MIB MiB (HBM counter calibration) and exit")
@@ -281,6 +343,9 @@ def main() -> int:
     if want("ulysses"):
         _log("ulysses share")
         secondary["ulysses_share"] = bench_ulysses(cea, torch, max(3, args.steps // 4), 1, dev)
+    if want("wire"):
+        _log("wire formats (Ulysses all-to-alls, packed distributed-KV merge)")
+        secondary["wire"] = bench_wire(cea, torch, args.steps, args.warmup, dev)
     if want("f32"):
         secondary["attn_f32_split"] = bench_f32_split(cea, torch, args.steps, args.warmup, dev)
     cpu = None

@@ -25,6 +25,8 @@ from .attention import (  # noqa: F401
     gqa_group,
     merge_attention,
     merge_attention_list,
+    merge_packed,
+    pack_partial,
     visibility_mask,
 )
 from .kv_cache import LayerKVCache, kv_append  # noqa: F401
@@ -36,6 +38,8 @@ from .sequence_parallel import (  # noqa: F401
     partitioned_attention,
     ring_attention,
     ulysses_attention,
+    ulysses_gather,
+    ulysses_scatter,
 )
 
 __version__ = "0.1.0"

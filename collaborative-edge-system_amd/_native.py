@@ -61,6 +61,13 @@ _SIGNATURES = {
     ),
     "cea_merge_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
     "cea_merge_attention_list": (ctypes.c_int, [ctypes.c_int32, _P, _P, _P, _P, ctypes.c_void_p]),
+    "cea_pack_partial": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p]),
+    "cea_merge_packed": (ctypes.c_int, [ctypes.c_int32, _P, _P, _P, ctypes.c_void_p]),
+    "cea_ulysses_scatter": (
+        ctypes.c_int,
+        [ctypes.c_int32, _P, _P, _P, _P] + [ctypes.c_int32] * 4 + [_P, _P, ctypes.c_void_p],
+    ),
+    "cea_ulysses_gather": (ctypes.c_int, [ctypes.c_int32, _P, ctypes.c_int64, _P, ctypes.c_void_p]),
     "cea_partitioned_attention_workspace_bytes": (
         ctypes.c_size_t,
         [ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)] + [ctypes.c_int64] * 5 + [ctypes.c_int32],

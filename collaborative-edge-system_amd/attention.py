@@ -277,6 +277,54 @@ def merge_attention_list(
     return _merge_list(outs, lses)
 
 
+def pack_partial(out: torch.Tensor, lse: torch.Tensor,
+                 packed: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The all-gather message of distributed-KV decoding: ``[B, Sq, H, D+1]`` holding ``out``
+    and, in the last slot, ``lse`` (sequence_parallel.py:275,
+    ``torch.cat([o, l.transpose(1, 2).unsqueeze(-1)], dim=-1)``).  ``packed`` may be a slot
+    of a preallocated gathered buffer ``[n, B, Sq, H, D+1]``."""
+    nat.require_device(out, lse, packed)
+    B, Sq, H, D = out.shape
+    if packed is None:
+        packed = torch.empty(B, Sq, H, D + 1, dtype=out.dtype, device=out.device)
+    out = _inner_contiguous(out)
+    lib = nat.load_library()
+    a = [nat.tensor_arg(t) for t in (out, lse, packed)]
+    rc = lib.cea_pack_partial(*(byref(x) for x in a), nat.stream_of(out.device))
+    nat.check(rc, "pack_partial")
+    return packed
+
+
+def merge_packed(gathered, out_dtype: Optional[torch.dtype] = None, return_lse: bool = False):
+    """Exact merge of all-gathered packed partials, read in place (sequence_parallel.py:277-280:
+    ``outs = [p[..., :D]]``, ``lses = [p[..., D].transpose(1, 2)]``, ``merge_attention_list``
+    and the cast to the query dtype).
+
+    ``gathered`` is the ``[n, B, Sq, H, D+1]`` buffer or a sequence of ``[B, Sq, H, D+1]``
+    parts; returns ``out`` in ``out_dtype`` (default the parts' dtype), plus the merged lse
+    when ``return_lse``."""
+    parts = list(gathered.unbind(0)) if isinstance(gathered, torch.Tensor) else list(gathered)
+    if not parts:
+        raise ValueError("need at least one packed partial")
+    nat.require_device(*parts)
+    parts = [_inner_contiguous(p) for p in parts]
+    B, Sq, H, D1 = parts[0].shape
+    dev = parts[0].device
+    if len(parts) > nat.MAX_PARTS:  # merge is associative: reduce in groups, then repack
+        groups = [merge_packed(parts[i : i + nat.MAX_PARTS], return_lse=True)
+                  for i in range(0, len(parts), nat.MAX_PARTS)]
+        parts = [pack_partial(o, l) for o, l in groups]
+    out = torch.empty(B, Sq, H, D1 - 1, dtype=out_dtype or parts[0].dtype, device=dev)
+    lse = torch.empty(B, H, Sq, dtype=parts[0].dtype, device=dev) if return_lse else None
+    lib = nat.load_library()
+    pa, oa = nat.tensor_array(parts), nat.tensor_arg(out)
+    la = nat.tensor_arg(lse) if lse is not None else None
+    rc = lib.cea_merge_packed(len(parts), pa, byref(oa), byref(la) if la is not None else None,
+                              nat.stream_of(dev))
+    nat.check(rc, "merge_packed")
+    return (out, lse) if return_lse else out
+
+
 def attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -315,5 +363,7 @@ __all__ = [
     "gqa_group",
     "merge_attention",
     "merge_attention_list",
+    "merge_packed",
+    "pack_partial",
     "visibility_mask",
 ]

@@ -534,6 +534,10 @@ bool prefill_mfma_supported(const AttnParams& p) {
   const int64_t kspan = ((int64_t)p.Sk - 1) * p.ks_s * 2 + p.D * 2;
   const int64_t vspan = ((int64_t)p.Sk - 1) * p.vs_s * 2 + p.D * 2;
   if (kspan >= ((int64_t)1 << 31) || vspan >= ((int64_t)1 << 31)) return false;
+  // the per-lane row offsets of a tile (up to 63 rows past its first key) must not wrap 32 bits
+  if ((int64_t)kTileKeys * p.ks_s * 2 >= ((int64_t)1 << 31) ||
+      (int64_t)kTileKeys * p.vs_s * 2 >= ((int64_t)1 << 31))
+    return false;
   return true;
 }
 

@@ -351,6 +351,210 @@ int cea_merge_attention_list(int32_t n, const cea_tensor* outs, const cea_tensor
   return merge_impl(n, outs, lses, out, lse, 0, (hipStream_t)stream);
 }
 
+int cea_merge_packed(int32_t n, const cea_tensor* parts, cea_tensor* out, cea_tensor* lse,
+                     void* stream) {
+  CEA_REQUIRE(parts && out, CEA_EINVAL, "merge_packed: missing tensor");
+  CEA_REQUIRE(n >= 1 && n <= CEA_MAX_PARTS, CEA_EUNSUPPORTED,
+              "merge_packed: between 1 and %d partial results supported, got %d", CEA_MAX_PARTS, n);
+  int rc;
+  if ((rc = check_tensor(&parts[0], "part_0", 4, -1, true))) return rc;
+  const int dt = parts[0].dtype;
+  CEA_REQUIRE(dt == CEA_F32 || dt == CEA_F64, CEA_EUNSUPPORTED,
+              "merge_packed: packed partials must be float32 or float64, got %s", dtype_name(dt));
+  CEA_REQUIRE(parts[0].size[3] >= 2, CEA_EINVAL, "merge_packed: rows must hold D values and the lse");
+  const int64_t D = parts[0].size[3] - 1;
+  const size_t esz = dtype_size(dt);
+  cea_tensor outs[CEA_MAX_PARTS], lses[CEA_MAX_PARTS];
+  for (int i = 0; i < n; ++i) {
+    const cea_tensor& t = parts[i];
+    if ((rc = check_tensor(&t, "part_i", 4, dt, true))) return rc;
+    for (int j = 0; j < 4; ++j)
+      CEA_REQUIRE(t.size[j] == parts[0].size[j], CEA_EINVAL,
+                  "merge_packed: partial %d has a different shape", i);
+    // out_i = part[..., :D];  lse_i = part[..., D].transpose(1, 2)
+    outs[i] = t;
+    outs[i].size[3] = D;
+    lses[i].data = (char*)t.data + D * esz;
+    lses[i].dtype = dt;
+    lses[i].ndim = 3;
+    lses[i].size[0] = t.size[0]; lses[i].size[1] = t.size[2]; lses[i].size[2] = t.size[1];
+    lses[i].stride[0] = t.stride[0]; lses[i].stride[1] = t.stride[2]; lses[i].stride[2] = t.stride[1];
+    lses[i].size[3] = 0; lses[i].stride[3] = 0;
+  }
+  return merge_impl(n, outs, lses, out, lse, 0, (hipStream_t)stream);
+}
+
+int cea_pack_partial(const cea_tensor* out, const cea_tensor* lse, cea_tensor* packed,
+                     void* stream) {
+  int rc;
+  if ((rc = check_tensor(out, "out", 4, -1, false))) return rc;
+  const int dt = out->dtype;
+  CEA_REQUIRE(dt == CEA_F32 || dt == CEA_F64, CEA_EUNSUPPORTED,
+              "pack_partial: partial results must be float32 or float64, got %s", dtype_name(dt));
+  if ((rc = check_tensor(lse, "lse", 3, dt, false))) return rc;
+  if ((rc = check_tensor(packed, "packed", 4, dt, true))) return rc;
+  const int64_t B = out->size[0], Sq = out->size[1], H = out->size[2], D = out->size[3];
+  CEA_REQUIRE(lse->size[0] == B && lse->size[1] == H && lse->size[2] == Sq, CEA_EINVAL,
+              "pack_partial: lse must be [B, H, Sq]");
+  CEA_REQUIRE(packed->size[0] == B && packed->size[1] == Sq && packed->size[2] == H &&
+                  packed->size[3] == D + 1,
+              CEA_EINVAL, "pack_partial: packed must be [B, Sq, H, D + 1]");
+  CEA_REQUIRE(D == 0 || out->stride[3] == 1, CEA_EINVAL, "pack_partial: innermost stride must be 1");
+  PackParams p;
+  memset(&p, 0, sizeof(p));
+  p.B = (int32_t)B; p.Sq = (int32_t)Sq; p.H = (int32_t)H; p.D = (int32_t)D;
+  p.dtype = dt;
+  p.out = out->data;
+  p.lse = lse->data;
+  p.packed = packed->data;
+  for (int j = 0; j < 3; ++j) {
+    p.os[j] = out->stride[j];
+    p.ls[j] = lse->stride[j];
+    p.ps[j] = packed->stride[j];
+  }
+  return launch_pack_partial(p, (hipStream_t)stream);
+}
+
+// 16 when every pointer, stride and length (bytes) is a multiple of 16, else the element size
+static int copy_vec(const int64_t* vals, int count, int esz) {
+  for (int i = 0; i < count; ++i)
+    if (vals[i] % 16) return esz;
+  return 16;
+}
+
+int cea_ulysses_scatter(int32_t n, const cea_tensor* qs, const cea_tensor* ks, const cea_tensor* vs,
+                        const cea_tensor* positions, int32_t q_start, int32_t q_count,
+                        int32_t kv_start, int32_t kv_count, cea_tensor* out, cea_tensor* pos_out,
+                        void* stream) {
+  CEA_REQUIRE(qs && ks && vs && out, CEA_EINVAL, "ulysses_scatter: missing tensor");
+  CEA_REQUIRE(n >= 1 && n <= CEA_MAX_PARTS, CEA_EUNSUPPORTED,
+              "ulysses_scatter: between 1 and %d ranks supported, got %d", CEA_MAX_PARTS, n);
+  CEA_REQUIRE((positions == nullptr) == (pos_out == nullptr), CEA_EINVAL,
+              "ulysses_scatter: positions and pos_out go together");
+  int rc;
+  if ((rc = check_tensor(out, "out", 4, -1, true))) return rc;
+  const int dt = out->dtype;
+  const int esz = (int)dtype_size(dt);
+  const int64_t B = out->size[0], S = out->size[1], W = out->size[2], D = out->size[3];
+  CEA_REQUIRE(q_count >= 0 && kv_count >= 0 && W == q_count + 2 * (int64_t)kv_count, CEA_EINVAL,
+              "ulysses_scatter: out must hold q_count + 2 * kv_count heads");
+  CEA_REQUIRE(W <= 1 || out->stride[2] == D, CEA_EINVAL,
+              "ulysses_scatter: the heads of an output token must be contiguous");
+  if (pos_out) {
+    if ((rc = check_tensor(pos_out, "pos_out", 2, CEA_I64, false))) return rc;
+    CEA_REQUIRE(pos_out->size[0] == B && pos_out->size[1] == S, CEA_EINVAL,
+                "ulysses_scatter: pos_out must be [B, S]");
+  }
+  UlyssesScatterParams p;
+  memset(&p, 0, sizeof(p));
+  p.n = n; p.B = (int32_t)B; p.S = (int32_t)S;
+  p.q_bytes = (int32_t)(q_count * D * esz);
+  p.kv_bytes = (int32_t)(kv_count * D * esz);
+  int64_t align[8 * CEA_MAX_PARTS + 6];
+  int na = 0;
+  int64_t tok = 0;
+  for (int j = 0; j < n; ++j) {
+    const cea_tensor* src[3] = {&qs[j], &ks[j], &vs[j]};
+    const int64_t start[3] = {q_start, kv_start, kv_start};
+    const int64_t count[3] = {q_count, kv_count, kv_count};
+    for (int c = 0; c < 3; ++c) {
+      if ((rc = check_tensor(src[c], c == 0 ? "q_j" : c == 1 ? "k_j" : "v_j", 4, dt, true))) return rc;
+      const cea_tensor* t = src[c];
+      CEA_REQUIRE(t->size[0] == B && t->size[1] == qs[j].size[1] && t->size[3] == D, CEA_EINVAL,
+                  "ulysses_scatter: shard %d shapes do not match the output", j);
+      CEA_REQUIRE(start[c] >= 0 && start[c] + count[c] <= t->size[2], CEA_EINVAL,
+                  "ulysses_scatter: head slice out of range for shard %d", j);
+      CEA_REQUIRE(count[c] <= 1 || t->stride[2] == D, CEA_EINVAL,
+                  "ulysses_scatter: the heads of a shard token must be contiguous");
+      const char* base = (const char*)t->data + start[c] * t->stride[2] * esz;
+      int64_t* st = c == 0 ? p.qs[j] : c == 1 ? p.ks[j] : p.vs[j];
+      st[0] = t->stride[0] * esz;
+      st[1] = t->stride[1] * esz;
+      if (c == 0) p.q[j] = base; else if (c == 1) p.k[j] = base; else p.v[j] = base;
+      align[na++] = (int64_t)(uintptr_t)base;
+      align[na++] = st[0];
+      align[na++] = st[1];
+    }
+    if (positions) {
+      if ((rc = check_tensor(&positions[j], "positions_j", 2, CEA_I64, false))) return rc;
+      CEA_REQUIRE(positions[j].size[0] == B && positions[j].size[1] == qs[j].size[1], CEA_EINVAL,
+                  "ulysses_scatter: positions of shard %d must be [B, s_j]", j);
+      p.pos[j] = (const int64_t*)positions[j].data;
+      p.ps[j][0] = positions[j].stride[0];
+      p.ps[j][1] = positions[j].stride[1];
+    }
+    p.tok_off[j] = (int32_t)tok;
+    tok += qs[j].size[1];
+  }
+  p.tok_off[n] = (int32_t)tok;
+  CEA_REQUIRE(tok == S, CEA_EINVAL, "ulysses_scatter: the shards hold %lld tokens, out has %lld",
+              (long long)tok, (long long)S);
+  p.out = (char*)out->data;
+  p.os_b = out->stride[0] * esz;
+  p.os_s = out->stride[1] * esz;
+  if (pos_out) {
+    p.pos_out = (int64_t*)pos_out->data;
+    p.pos_b = pos_out->stride[0];
+    p.pos_s = pos_out->stride[1];
+  }
+  align[na++] = (int64_t)(uintptr_t)p.out;
+  align[na++] = p.os_b;
+  align[na++] = p.os_s;
+  align[na++] = p.q_bytes;
+  align[na++] = p.kv_bytes;
+  return launch_ulysses_scatter(p, copy_vec(align, na, esz), (hipStream_t)stream);
+}
+
+int cea_ulysses_gather(int32_t n, const cea_tensor* outs, int64_t token_start, cea_tensor* out,
+                       void* stream) {
+  CEA_REQUIRE(outs && out, CEA_EINVAL, "ulysses_gather: missing tensor");
+  CEA_REQUIRE(n >= 1 && n <= CEA_MAX_PARTS, CEA_EUNSUPPORTED,
+              "ulysses_gather: between 1 and %d ranks supported, got %d", CEA_MAX_PARTS, n);
+  int rc;
+  if ((rc = check_tensor(out, "out", 4, -1, true))) return rc;
+  const int dt = out->dtype;
+  const int esz = (int)dtype_size(dt);
+  const int64_t B = out->size[0], S = out->size[1], H = out->size[2], D = out->size[3];
+  CEA_REQUIRE(H <= 1 || out->stride[2] == D, CEA_EINVAL,
+              "ulysses_gather: the heads of an output token must be contiguous");
+  UlyssesGatherParams p;
+  memset(&p, 0, sizeof(p));
+  p.n = n; p.B = (int32_t)B; p.S = (int32_t)S;
+  int64_t align[4 * CEA_MAX_PARTS + 3];
+  int na = 0;
+  int64_t heads = 0;
+  for (int j = 0; j < n; ++j) {
+    const cea_tensor* t = &outs[j];
+    if ((rc = check_tensor(t, "outs_j", 4, dt, true))) return rc;
+    CEA_REQUIRE(t->size[0] == B && t->size[3] == D, CEA_EINVAL,
+                "ulysses_gather: head output %d does not match the output", j);
+    CEA_REQUIRE(token_start >= 0 && token_start + S <= t->size[1], CEA_EINVAL,
+                "ulysses_gather: tokens [%lld, %lld) outside head output %d", (long long)token_start,
+                (long long)(token_start + S), j);
+    CEA_REQUIRE(t->size[2] <= 1 || t->stride[2] == D, CEA_EINVAL,
+                "ulysses_gather: the heads of a source token must be contiguous");
+    p.src[j] = (const char*)t->data + token_start * t->stride[1] * esz;
+    p.ss[j][0] = t->stride[0] * esz;
+    p.ss[j][1] = t->stride[1] * esz;
+    p.bytes[j] = (int32_t)(t->size[2] * D * esz);
+    p.dst_off[j] = (int32_t)(heads * D * esz);
+    heads += t->size[2];
+    align[na++] = (int64_t)(uintptr_t)p.src[j];
+    align[na++] = p.ss[j][0];
+    align[na++] = p.ss[j][1];
+    align[na++] = p.bytes[j];
+  }
+  CEA_REQUIRE(heads == H, CEA_EINVAL, "ulysses_gather: head outputs hold %lld heads, out has %lld",
+              (long long)heads, (long long)H);
+  p.out = (char*)out->data;
+  p.os_b = out->stride[0] * esz;
+  p.os_s = out->stride[1] * esz;
+  align[na++] = (int64_t)(uintptr_t)p.out;
+  align[na++] = p.os_b;
+  align[na++] = p.os_s;
+  return launch_ulysses_gather(p, copy_vec(align, na, esz), (hipStream_t)stream);
+}
+
 size_t cea_partitioned_attention_workspace_bytes(int32_t n, const int64_t* Sk, int64_t B,
                                                  int64_t Sq, int64_t Hq, int64_t Hkv, int64_t D,
                                                  int32_t in_dtype) {

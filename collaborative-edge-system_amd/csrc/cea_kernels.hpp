@@ -91,7 +91,51 @@ struct DecodeParams {
   int32_t accumulate;
 };
 
+// Packing of one partial result into the all-gather message [B,Sq,H,D+1] (out | lse).
+struct PackParams {
+  int32_t B, Sq, H, D;
+  int32_t dtype;             // CEA_F32 or CEA_F64
+  const void* out;
+  int64_t os[3];             // b, s, h element strides
+  const void* lse;
+  int64_t ls[3];             // b, h, s
+  void* packed;
+  int64_t ps[3];             // b, s, h
+};
+
+// First Ulysses all-to-all seen from one rank: n source shards -> [B, S, width, D].  Pointers
+// are bytes, already offset to the first head of the slice; strides are bytes (b, s).
+struct UlyssesScatterParams {
+  int32_t n, B, S;
+  int32_t tok_off[CEA_MAX_PARTS + 1];  // first token of each source in the output
+  const char* q[CEA_MAX_PARTS];
+  const char* k[CEA_MAX_PARTS];
+  const char* v[CEA_MAX_PARTS];
+  int64_t qs[CEA_MAX_PARTS][2], ks[CEA_MAX_PARTS][2], vs[CEA_MAX_PARTS][2];
+  const int64_t* pos[CEA_MAX_PARTS];   // element strides (b, s); may be null with pos_out
+  int64_t ps[CEA_MAX_PARTS][2];
+  int32_t q_bytes, kv_bytes;            // bytes of the q slice / of each kv slice per token
+  char* out;
+  int64_t os_b, os_s;
+  int64_t* pos_out;
+  int64_t pos_b, pos_s;
+};
+
+// Second Ulysses all-to-all seen from one rank: n head outputs -> [B, S_r, H, D].
+struct UlyssesGatherParams {
+  int32_t n, B, S;
+  const char* src[CEA_MAX_PARTS];      // offset to the rank's first token
+  int64_t ss[CEA_MAX_PARTS][2];        // bytes (b, s)
+  int32_t bytes[CEA_MAX_PARTS];        // bytes per token of source j
+  int32_t dst_off[CEA_MAX_PARTS];      // their offset in an output token row
+  char* out;
+  int64_t os_b, os_s;
+};
+
 int launch_merge(const MergeParams& p, hipStream_t s);
+int launch_pack_partial(const PackParams& p, hipStream_t s);
+int launch_ulysses_scatter(const UlyssesScatterParams& p, int vec, hipStream_t s);
+int launch_ulysses_gather(const UlyssesGatherParams& p, int vec, hipStream_t s);
 int launch_rmsnorm(const cea_tensor* x, const cea_tensor* w, double eps, cea_tensor* y,
                    hipStream_t s);
 int launch_rope_tables(const cea_tensor* pos, const cea_tensor* inv, cea_tensor* c,

@@ -39,6 +39,8 @@ from .attention import (
     attention_with_lse,
     attention_with_lse_into,
     merge_attention_list,
+    merge_packed,
+    pack_partial,
 )
 from .partition import HeadShard, SequenceLayout, offsets_of
 
@@ -246,15 +248,31 @@ def distributed_kv_attention(
     scale: Optional[float] = None,
     kv_map: KVMap = None,
     kv_block: Optional[int] = None,
+    wire: bool = False,
 ) -> torch.Tensor:
     """A replicated query against a KV cache sharded over the ranks of ``comm``
-    (sequence_parallel.py:250-280); returns ``[B, Sq, Hq, D]`` in ``q.dtype``."""
+    (sequence_parallel.py:250-280); returns ``[B, Sq, Hq, D]`` in ``q.dtype``.
+
+    By default every rank's partition runs in one split-KV launch with the merge in its
+    reduction.  ``wire=True`` runs the multi-device data flow instead: each rank's partial
+    ``(out, lse)`` is packed into its slot of the all-gathered ``[n, B, Sq, H, D+1]`` buffer
+    (the message layout of sequence_parallel.py:275-276) and the buffer is merged in place
+    (:277-280)."""
     if comm.size == 1:
         o, _ = attention_with_lse(q, k_local, v_local, q_pos, k_pos_local, causal=causal,
                                   scale=scale, kv_map=kv_map, kv_block=kv_block)
         return o.to(q.dtype)
     own = (k_local, v_local, k_pos_local)
     parts = [_kv_from(comm, i, own) for i in range(comm.size)]  # rank order, as all_gather
+    if wire:
+        B, Sq, Hq, D = q.shape
+        gathered = torch.empty(comm.size, B, Sq, Hq, D + 1, dtype=accumulation_dtype(q.dtype),
+                               device=q.device)
+        for i, (kk, vv, pp) in enumerate(parts):
+            o, l = attention_with_lse(q, kk, vv, q_pos, pp, causal=causal, scale=scale,
+                                      kv_map=kv_map, kv_block=kv_block)
+            pack_partial(o, l, gathered[i])
+        return merge_packed(gathered, out_dtype=q.dtype)
     if kv_block is not None:
         partial = [attention_with_lse(q, kk, vv, q_pos, pp, causal=causal, scale=scale,
                                       kv_map=kv_map, kv_block=kv_block) for kk, vv, pp in parts]
@@ -274,14 +292,28 @@ def _check_ulysses(comm: LocalGroup, seq_sizes: Sequence[int], head_shards: Sequ
         raise ValueError("need one head shard per rank")
 
 
+def _heads_contiguous(t: torch.Tensor) -> torch.Tensor:
+    """``t`` with the heads of a token adjacent in memory (the copy kernels move whole token
+    rows); a copy only for views that break this."""
+    if t.shape[2] > 1 and t.stride(2) != t.shape[3] or t.stride(3) != 1 and t.shape[3] > 1:
+        return t.contiguous()
+    return t
+
+
 def ulysses_scatter(q, k, v, positions, comm: LocalGroup, seq_sizes: Sequence[int],
                     head_shards: Sequence[HeadShard]):
     """Sequence-sharded -> head-sharded (sequence_parallel.py:143-179): this rank's heads over
-    the whole sequence, tokens concatenated in rank order, with their positions ``[B, S]``."""
+    the whole sequence, tokens concatenated in rank order, with their positions ``[B, S]``.
+
+    Every rank's shard is read where it lies and packed by one kernel
+    (``cea_ulysses_scatter``) into this rank's receive buffer ``[B, S, q+2kv heads, D]``;
+    ``q_f``, ``k_f``, ``v_f`` are head slices of it, as the reference's ``split`` returns.
+    With wire compression every piece travels rounded through the wire dtype, as
+    ``all_to_all(..., compress=True)`` does (distributed/comm.py:468-486)."""
     n, r = comm.size, comm.rank
     _check_ulysses(comm, seq_sizes, head_shards, q.shape[1])
     me = head_shards[r]
-    qs, ks, vs, ps = [], [], [], []
+    shards = []
     for j in range(n):
         if j == r:
             sq, sk, sv, sp = q, k, v, positions
@@ -290,23 +322,48 @@ def ulysses_scatter(q, k, v, positions, comm: LocalGroup, seq_sizes: Sequence[in
             sq, sk, sv, sp = s["q"], s["k"], s["v"], s["pos"]
             if sq.shape[1] != seq_sizes[j]:
                 raise ValueError(f"seq_sizes {list(seq_sizes)} inconsistent with rank {j}")
-        qs.append(sq[:, :, me.q_start : me.q_start + me.q_count])
-        ks.append(sk[:, :, me.kv_start : me.kv_start + me.kv_count])
-        vs.append(sv[:, :, me.kv_start : me.kv_start + me.kv_count])
-        ps.append(sp)
-    cat = (lambda xs: torch.cat(xs, dim=1)) if n > 1 else (lambda xs: xs[0])
-    return cat(qs), cat(ks), cat(vs), cat(ps)
+        if comm.wire_dtype is not None and n > 1:
+            sq, sk, sv = (x.to(comm.wire_dtype).to(x.dtype) for x in (sq, sk, sv))
+        shards.append((_heads_contiguous(sq), _heads_contiguous(sk), _heads_contiguous(sv),
+                       _positions(sp)))
+    nat.require_device(*[t for sh in shards for t in sh])
+    B, _, _, D = q.shape
+    S = sum(sh[0].shape[1] for sh in shards)
+    width = me.q_count + 2 * me.kv_count
+    full = torch.empty(B, S, width, D, dtype=q.dtype, device=q.device)
+    pos_f = torch.empty(B, S, dtype=torch.int64, device=q.device)
+    lib = nat.load_library()
+    qa, ka, va, pa = (nat.tensor_array([sh[i] for sh in shards]) for i in range(4))
+    fa, pfa = nat.tensor_arg(full), nat.tensor_arg(pos_f)
+    rc = lib.cea_ulysses_scatter(n, qa, ka, va, pa, me.q_start, me.q_count, me.kv_start,
+                                 me.kv_count, byref(fa), byref(pfa), nat.stream_of(q.device))
+    nat.check(rc, "ulysses_scatter")
+    q_f, k_f, v_f = full.split([me.q_count, me.kv_count, me.kv_count], dim=2)
+    return q_f, k_f, v_f, pos_f
 
 
 def ulysses_gather(out_heads_of_ranks: Sequence[torch.Tensor], comm: LocalGroup,
                    seq_sizes: Sequence[int], head_shards: Sequence[HeadShard]) -> torch.Tensor:
     """Head-sharded -> sequence-sharded (sequence_parallel.py:182-194).  On one GPU every
     rank's head output ``[B, S, h_j, D]`` is available; returns this rank's tokens with all
-    heads ``[B, s_r, H, D]``."""
+    heads ``[B, s_r, H, D]``, built by one kernel (``cea_ulysses_gather``)."""
     r = comm.rank
+    outs = list(out_heads_of_ranks)
+    if len(outs) != comm.size:
+        raise ValueError("need one head output per rank")
+    if comm.wire_dtype is not None and comm.size > 1:
+        outs = [o.to(comm.wire_dtype).to(o.dtype) for o in outs]
+    outs = [_heads_contiguous(o) for o in outs]
+    nat.require_device(*outs)
     start = offsets_of(seq_sizes)[r]
-    pieces = [o[:, start : start + seq_sizes[r]] for o in out_heads_of_ranks]
-    return torch.cat(pieces, dim=2) if len(pieces) > 1 else pieces[0]
+    B, _, _, D = outs[0].shape
+    H = sum(o.shape[2] for o in outs)
+    res = torch.empty(B, seq_sizes[r], H, D, dtype=outs[0].dtype, device=outs[0].device)
+    lib = nat.load_library()
+    oa, ra = nat.tensor_array(outs), nat.tensor_arg(res)
+    rc = lib.cea_ulysses_gather(len(outs), oa, int(start), byref(ra), nat.stream_of(res.device))
+    nat.check(rc, "ulysses_gather")
+    return res
 
 
 def ulysses_attention(

@@ -107,6 +107,61 @@ int cea_merge_attention_list(int32_t n, const cea_tensor* outs, const cea_tensor
                              cea_tensor* out, cea_tensor* lse, void* stream);
 
 /*
+ * Packs one partial result into the all-gather message of distributed-KV decoding:
+ * packed[..., :D] = out, packed[..., D] = lse transposed to [B,Sq,H].
+ * Replaces torch.cat([o, l.transpose(1, 2).unsqueeze(-1)], dim=-1)
+ * (collab_infer/parallel/sequence_parallel.py:275).
+ *   out [B,Sq,H,D] f32/f64 (innermost stride 1), lse [B,H,Sq] same dtype,
+ *   packed [B,Sq,H,D+1] same dtype (innermost stride 1), e.g. one rank's slot of the
+ *   gathered [n,B,Sq,H,D+1] buffer.
+ */
+int cea_pack_partial(const cea_tensor* out, const cea_tensor* lse, cea_tensor* packed,
+                     void* stream);
+
+/*
+ * Exact merge of n packed partial results read in place from the all-gathered buffer:
+ * out_i = part_i[..., :D], lse_i = part_i[..., D] transposed to [B,H,Sq], merged like
+ * cea_merge_attention_list and written in out's dtype.
+ * Replaces the unpacking and merge after the all-gather of distributed_kv_attention,
+ * `outs = [p[..., :D]]; lses = [p[..., D].transpose(1, 2)]; merge_attention_list(outs, lses)`
+ * and the final `.to(q.dtype)` (collab_infer/parallel/sequence_parallel.py:277-280).
+ *   parts  n tensors [B,Sq,H,D+1] f32/f64 (innermost stride 1), e.g. views of the gathered
+ *          [n,B,Sq,H,D+1] buffer;  out [B,Sq,H,D] the parts' dtype, or bf16/f16 from f32;
+ *   lse    [B,H,Sq] the parts' dtype, or NULL.
+ */
+int cea_merge_packed(int32_t n, const cea_tensor* parts, cea_tensor* out, cea_tensor* lse,
+                     void* stream);
+
+/*
+ * First Ulysses all-to-all as seen by one rank, on one device: the n ranks' sequence shards
+ * q_j [B,s_j,Hq,D], k_j / v_j [B,s_j,Hkv,D] contribute this rank's heads
+ * q[:, :, q_start:q_start+q_count], k/v[:, :, kv_start:kv_start+kv_count], packed per token
+ * as [q heads | k heads | v heads] and concatenated over the ranks' tokens in rank order;
+ * positions_j [B,s_j] are all-gathered the same way.
+ * Replaces the send-side slicing, concatenation and .contiguous(), the all_to_all plus
+ * torch.cat(received, dim=1), and the positions all_gather of ulysses_scatter
+ * (collab_infer/parallel/sequence_parallel.py:163-178); q_f, k_f, v_f are the head slices
+ * [0,q_count), [q_count, q_count+kv_count), [q_count+kv_count, width) of out.
+ *   out [B,S,q_count+2*kv_count,D] (S = sum s_j, heads of a token contiguous), all shards in
+ *   out's dtype with the heads of a token contiguous;  positions / pos_out [B,S] i64 both
+ *   given or both NULL.
+ */
+int cea_ulysses_scatter(int32_t n, const cea_tensor* qs, const cea_tensor* ks, const cea_tensor* vs,
+                        const cea_tensor* positions, int32_t q_start, int32_t q_count,
+                        int32_t kv_start, int32_t kv_count, cea_tensor* out, cea_tensor* pos_out,
+                        void* stream);
+
+/*
+ * Second Ulysses all-to-all as seen by one rank, on one device: tokens
+ * [token_start, token_start + S_r) of every rank's head output outs_j [B,S,h_j,D],
+ * concatenated over heads in rank order into out [B,S_r,sum h_j,D].
+ * Replaces the per-destination slicing, the all_to_all and torch.cat(back, dim=2) of
+ * ulysses_gather (collab_infer/parallel/sequence_parallel.py:182-194).
+ */
+int cea_ulysses_gather(int32_t n, const cea_tensor* outs, int64_t token_start, cea_tensor* out,
+                       void* stream);
+
+/*
  * Attention of one query block against n KV partitions plus the exact merge, in one pass:
  * the per-device compute of distributed_kv_attention
  * (collab_infer/parallel/sequence_parallel.py:250-280) for n simulated ranks, with the

@@ -50,6 +50,47 @@ def distributed_kv_share(q, q_pos, parts, *, causal=True, scale=None, kv_map=Non
     return (res, lse, partial) if with_parts else res
 
 
+def pack_partial(out, lse):
+    """sequence_parallel.py:275: the all-gather message ``[B, Sq, H, D+1]`` (out | lse)."""
+    return torch.cat([out, lse.transpose(1, 2).unsqueeze(-1)], dim=-1)
+
+
+def merge_packed(parts, out_dtype):
+    """sequence_parallel.py:277-280: unpack every gathered message, merge in rank order,
+    cast to the query dtype."""
+    D = parts[0].shape[-1] - 1
+    outs = [p[..., :D] for p in parts]
+    lses = [p[..., D].transpose(1, 2) for p in parts]
+    out, _ = merge_many(outs, lses) if len(parts) > 1 else (outs[0], lses[0])
+    return out.to(out_dtype)
+
+
+def ulysses_scatter(shards, head_shards, rank: int):
+    """sequence_parallel.py:163-178 for rank ``rank``.  ``shards[j] = (q_j, k_j, v_j, pos_j)``
+    is rank j's sequence shard; the all_to_all delivers to ``rank`` what every rank j puts in
+    its send list at index ``rank``.  Returns ``(q_f, k_f, v_f, pos_f)``."""
+    received = []
+    for q, k, v, _ in shards:  # what rank j sends
+        sends = [torch.cat([q[:, :, sh.q_start : sh.q_start + sh.q_count],
+                            k[:, :, sh.kv_start : sh.kv_start + sh.kv_count],
+                            v[:, :, sh.kv_start : sh.kv_start + sh.kv_count]], dim=2).contiguous()
+                 for sh in head_shards]
+        received.append(sends[rank])
+    full = torch.cat(received, dim=1) if len(shards) > 1 else received[0]
+    me = head_shards[rank]
+    q_f, k_f, v_f = full.split([me.q_count, me.kv_count, me.kv_count], dim=2)
+    pos_f = torch.cat([s[3] for s in shards], dim=1)
+    return q_f, k_f, v_f, pos_f
+
+
+def ulysses_gather(out_heads, seq_sizes: Sequence[int], rank: int):
+    """sequence_parallel.py:182-194 for rank ``rank``: ``out_heads[j]`` is rank j's head output
+    over the whole sequence; rank j sends token slice i to rank i."""
+    starts = [sum(seq_sizes[:i]) for i in range(len(seq_sizes))]
+    back = [o[:, starts[rank] : starts[rank] + seq_sizes[rank]].contiguous() for o in out_heads]
+    return torch.cat(back, dim=2) if len(back) > 1 else back[0]
+
+
 def ulysses_local(q_f, k_f, v_f, pos_f, kv_map=None, *, causal=True, scale=None):
     """sequence_parallel.py:237: the head-sharded local attention after the scatter."""
     return plain_attention(q_f, k_f, v_f, pos_f, pos_f, causal=causal, scale=scale, kv_map=kv_map)

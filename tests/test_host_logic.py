@@ -177,3 +177,117 @@ def test_oracle_shares_match_single_device(world, kind, weights, causal):
     # the brute force agrees with the single-device result too
     bo, _ = _brute.attention(q, k, v, pos, pos, causal)
     assert (torch.from_numpy(bo) - full)[valid].abs().max().item() < 1e-12
+
+
+# ---- wire formats: packed partials and the Ulysses all-to-alls (oracle pins) -----------------
+
+def _shards(world, weights, kind, dtype=torch.float64, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, S, HQ, D, generator=g, dtype=dtype)
+    k = torch.randn(B, S, HKV, D, generator=g, dtype=dtype)
+    v = torch.randn(B, S, HKV, D, generator=g, dtype=dtype)
+    pos = torch.arange(S).repeat(B, 1)
+    layout = P.SequenceLayout(S, world, weights, kind)
+    shards = [(layout.shard(q, r), layout.shard(k, r), layout.shard(v, r), layout.shard(pos, r))
+              for r in range(world)]
+    return q, k, v, pos, layout, shards
+
+
+def _scatter_pin(scatter, world, weights, kind):
+    """Rank r's scattered q/k/v are its head slices of the rank-order concatenation of the
+    shards, and its positions that concatenation's positions (sequence_parallel.py:163-178)."""
+    q, k, v, pos, layout, shards = _shards(world, weights, kind)
+    heads = P.partition_heads(HQ, HKV, weights or world)
+    cat = lambda i: torch.cat([s[i] for s in shards], dim=1)  # noqa: E731
+    for r, sh in enumerate(heads):
+        q_f, k_f, v_f, pos_f = scatter(shards, heads, r)
+        if not (torch.equal(q_f, cat(0)[:, :, sh.q_start:sh.q_start + sh.q_count])
+                and torch.equal(k_f, cat(1)[:, :, sh.kv_start:sh.kv_start + sh.kv_count])
+                and torch.equal(v_f, cat(2)[:, :, sh.kv_start:sh.kv_start + sh.kv_count])
+                and torch.equal(pos_f, cat(3))):
+            return False
+    return True
+
+
+def _gather_pin(gather, world, weights, kind):
+    """Gathering every rank's head slice of a full tensor returns each rank's own token shard
+    with all heads (sequence_parallel.py:182-194)."""
+    q, _, _, _, layout, shards = _shards(world, weights, kind)
+    heads = P.partition_heads(HQ, HKV, weights or world)
+    full = torch.cat([s[0] for s in shards], dim=1)
+    outs = [full[:, :, sh.q_start:sh.q_start + sh.q_count] for sh in heads]
+    return all(torch.equal(gather(outs, layout.sizes, r), shards[r][0]) for r in range(world))
+
+
+@pytest.mark.parametrize("world,weights,kind", [(2, None, "contiguous"), (3, [3, 2, 1], "zigzag"),
+                                                (4, [1, 1, 2, 3], "contiguous")])
+def test_oracle_ulysses_scatter_gather_pins(world, weights, kind):
+    assert _scatter_pin(sp_ref.ulysses_scatter, world, weights, kind)
+    assert _gather_pin(sp_ref.ulysses_gather, world, weights, kind)
+
+
+@pytest.mark.parametrize("world,weights,kind,causal", [(2, None, "contiguous", True),
+                                                       (3, [3, 2, 1], "zigzag", True),
+                                                       (3, [1, 2, 3], "contiguous", False)])
+def test_oracle_ulysses_end_to_end_matches_single_device(world, weights, kind, causal):
+    """Scatter -> per-rank local attention -> gather == single-device attention of each rank's
+    tokens (the reference's tests/test_sequence_parallel.py:29-67, < 1e-12 in f64)."""
+    q, k, v, pos, layout, shards = _shards(world, weights, kind)
+    pos[1, -4:] = -1  # right padding of one sequence
+    shards = [(s[0], s[1], s[2], layout.shard(pos, r)) for r, s in enumerate(shards)]
+    full = ref.plain_attention(q, k, v, pos, pos, causal=causal)
+    heads = P.partition_heads(HQ, HKV, weights or world)
+    outs = []
+    for r, sh in enumerate(heads):
+        q_f, k_f, v_f, pos_f = sp_ref.ulysses_scatter(shards, heads, r)
+        outs.append(sp_ref.ulysses_local(q_f, k_f, v_f, pos_f, sh.kv_map, causal=causal))
+    for r in range(world):
+        mine = sp_ref.ulysses_gather(outs, layout.sizes, r)
+        want = layout.shard(full, r)
+        valid = layout.shard(pos, r) >= 0
+        assert (mine - want)[valid].abs().max().item() < 1e-12
+
+
+def test_oracle_packed_merge_matches_single_device():
+    """Partials of disjoint KV partitions, packed into the all-gather message and merged from
+    it, equal single-device attention (sequence_parallel.py:270-280, < 1e-12 in f64); the
+    message holds out and lse unchanged."""
+    q, k, v, pos = _inputs()
+    full = ref.plain_attention(q, k, v, pos, pos)
+    cuts = [0, 4, 9, S]
+    parts = []
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        o, l = ref.attention_with_lse(q, k[:, a:b], v[:, a:b], pos, pos[:, a:b])
+        pk = sp_ref.pack_partial(o, l)
+        assert pk.shape == (B, S, HQ, D + 1)
+        assert torch.equal(pk[..., :D], o) and torch.equal(pk[..., D], l.transpose(1, 2))
+        parts.append(pk)
+    merged = sp_ref.merge_packed(parts, torch.float64)
+    valid = pos >= 0
+    assert (merged - full)[valid].abs().max().item() < 1e-12
+
+
+def test_wire_pins_reject_planted_mistakes():
+    """Each pin above fails for a plausible mistake in the restatement."""
+    def scatter_kqv(shards, heads, r):  # heads packed in the wrong order
+        q_f, k_f, v_f, pos_f = sp_ref.ulysses_scatter(shards, heads, r)
+        return q_f, v_f, k_f, pos_f
+
+    def scatter_reversed(shards, heads, r):  # tokens concatenated in reverse rank order
+        return sp_ref.ulysses_scatter(shards[::-1], heads, r)
+
+    def gather_reversed(outs, sizes, r):  # head outputs concatenated in reverse rank order
+        return sp_ref.ulysses_gather(outs[::-1], sizes, r)
+
+    assert not _scatter_pin(scatter_kqv, 2, None, "contiguous")
+    assert not _scatter_pin(scatter_reversed, 3, [3, 2, 1], "zigzag")
+    assert not _gather_pin(gather_reversed, 3, [3, 2, 1], "zigzag")
+    # an lse packed without the transpose breaks the merge for Sq > 1, H > 1
+    q, k, v, pos = _inputs()
+    full = ref.plain_attention(q, k, v, pos, pos)
+    parts = []
+    for a, b in ((0, 6), (6, S)):
+        o, l = ref.attention_with_lse(q, k[:, a:b], v[:, a:b], pos, pos[:, a:b])
+        parts.append(torch.cat([o, l.reshape(B, S, HQ, 1)], dim=-1))
+    merged = sp_ref.merge_packed(parts, torch.float64)
+    assert (merged - full)[pos >= 0].abs().max().item() > 1e-3
