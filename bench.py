@@ -342,7 +342,7 @@ def main() -> int:
         secondary["kv_append"] = bench_kv_append(cea, torch, args.steps, args.warmup, dev)
     if want("ulysses"):
         _log("ulysses share")
-        secondary["ulysses_share"] = bench_ulysses(cea, torch, max(3, args.steps // 4), 1, dev)
+        secondary["ulysses_share"] = bench_ulysses(cea, torch, max(5, args.steps // 2), args.warmup, dev)
     if want("wire"):
         _log("wire formats (Ulysses all-to-alls, packed distributed-KV merge)")
         secondary["wire"] = bench_wire(cea, torch, args.steps, args.warmup, dev)
