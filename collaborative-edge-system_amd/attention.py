@@ -206,6 +206,7 @@ def attention_with_lse_into(
     scale: Optional[float] = None,
     kv_map: KVMap = None,
     accumulate: bool = True,
+    final: Optional[torch.Tensor] = None,
 ) -> None:
     """Merges attention over one more KV block into a running ``(out, lse)`` in place.
 
@@ -215,15 +216,35 @@ def attention_with_lse_into(
     ``out = 0``, ``lse = -inf`` (the merge's neutral element), or pass
     ``accumulate=False`` for the first block: its result then overwrites ``(out, lse)``,
     which need no initialisation (an empty block leaves them untouched either way).
+
+    ``final`` (``[B, Sq, Hq, D]`` in q's dtype or the accumulation dtype) receives the merged
+    output instead of ``out`` - the last step of a ring with its ``out.to(q.dtype)``
+    (sequence_parallel.py:121, 128) in the same kernel; ``out`` is then left unspecified.
     """
-    if k.shape[1] == 0 or q.shape[1] == 0:
+    if final is not None and not accumulate:
+        raise ValueError("final needs accumulate=True")
+    if q.shape[1] == 0 or (k.shape[1] == 0 and final is None):
         return
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
     q, k, v, q_pos, k_pos, mapping = _prepare(q, k, v, q_pos, k_pos, kv_map)
     acc = accumulation_dtype(q.dtype)
     if out.dtype != acc or lse.dtype != acc:
         raise ValueError(f"running (out, lse) must be {acc}")
-    _launch(q, k, v, q_pos, k_pos, causal, scale, mapping, out, lse, bool(accumulate))
+    if final is None:
+        _launch(q, k, v, q_pos, k_pos, causal, scale, mapping, out, lse, bool(accumulate))
+        return
+    nat.require_device(final)
+    lib = nat.load_library()
+    B, Sq, Hq, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    ws = nat.workspace(lib.cea_attention_workspace_bytes(B, Sq, Hq, Sk, Hkv, D,
+                                                         nat.DTYPE_CODES[q.dtype]), q.device)
+    km, kn = nat.kv_map_arg(mapping)
+    args = [nat.tensor_arg(t) for t in (q, k, v, q_pos, k_pos, out, lse, final)]
+    rc = lib.cea_attention_merge_final(
+        *(byref(a) for a in args[:5]), int(bool(causal)), float(scale), km, kn,
+        *(byref(a) for a in args[5:]), ws.data_ptr(), ws.numel(), nat.stream_of(q.device))
+    nat.check(rc, "attention_merge_final")
 
 
 def merge_attention(

@@ -440,19 +440,34 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     const float safe = is_finite(lse) ? lse : 0.f;
     const float w_old = expf(lse_old - safe), w_new = expf(lse_new - safe);
     float* orow = (float*)p.out + b * p.os_b + (int64_t)row * p.os_s + h * p.os_h;
+    // the last merge of a ring can write the result in the query dtype straight away (the
+    // reference's final out.to(q.dtype)); the running output is then only read
+    T* frow = p.final_out && p.final_dtype != CEA_F32
+                  ? (T*)p.final_out + b * p.fs_b + (int64_t)row * p.fs_s + h * p.fs_h
+                  : nullptr;
+    float* ffrow = p.final_out && p.final_dtype == CEA_F32
+                       ? (float*)p.final_out + b * p.fs_b + (int64_t)row * p.fs_s + h * p.fs_h
+                       : orow;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
-        float4* dst = (float4*)(orow + dt * 32 + i4 * 8 + g * 4);
-        float4 prev = *dst;
+        const int col = dt * 32 + i4 * 8 + g * 4;
+        float4 prev = *(const float4*)(orow + col);
         const float o0 = oacc[dt][i4 * 4 + 0] * inv, o1 = oacc[dt][i4 * 4 + 1] * inv;
         const float o2 = oacc[dt][i4 * 4 + 2] * inv, o3 = oacc[dt][i4 * 4 + 3] * inv;
         prev.x = add_rn(mul_rn(prev.x, w_old), mul_rn(o0, w_new));
         prev.y = add_rn(mul_rn(prev.y, w_old), mul_rn(o1, w_new));
         prev.z = add_rn(mul_rn(prev.z, w_old), mul_rn(o2, w_new));
         prev.w = add_rn(mul_rn(prev.w, w_old), mul_rn(o3, w_new));
-        *dst = prev;
+        if (frow) {
+          const T v4[4] = {(T)prev.x, (T)prev.y, (T)prev.z, (T)prev.w};
+          uint2 raw;
+          __builtin_memcpy(&raw, v4, 8);
+          *(uint2*)(frow + col) = raw;
+        } else {
+          *(float4*)(ffrow + col) = prev;
+        }
       }
     // both halves have read lse_old before either writes it
     __builtin_amdgcn_wave_barrier();
@@ -515,6 +530,11 @@ bool prefill_mfma_supported(const AttnParams& p) {
   if (!(p.D == 64 || p.D == 128)) return false;
   if (!(p.out_dtype == CEA_F32 || p.out_dtype == p.in_dtype)) return false;
   if (p.accumulate && p.out_dtype != CEA_F32) return false;
+  if (p.final_out) {
+    if (!(p.final_dtype == CEA_F32 || p.final_dtype == p.in_dtype)) return false;
+    if (p.fs_b % 4 || p.fs_s % 4 || p.fs_h % 4) return false;
+    if (((uintptr_t)p.final_out & 15) != 0) return false;
+  }
   // the exp2 fold needs c = |scale|*log2(e) to be a normal f32 (a zero c would turn the
   // -inf of masked scores into NaN); degenerate scales use the generic kernel
   if (!(fabs(p.scale) >= 1e-30 && fabs(p.scale) <= 1e30)) return false;

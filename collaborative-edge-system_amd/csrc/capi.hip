@@ -280,6 +280,40 @@ int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_t
   return run_attention(p, (char*)workspace, workspace_bytes, (hipStream_t)stream);
 }
 
+static int merge_impl(int32_t n, const cea_tensor* outs, const cea_tensor* lses, cea_tensor* out,
+                      cea_tensor* lse, int pairwise, hipStream_t st);
+
+int cea_attention_merge_final(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
+                              const cea_tensor* q_pos, const cea_tensor* k_pos, int32_t causal,
+                              double scale, const int32_t* kv_map, int32_t kv_map_len,
+                              cea_tensor* out, cea_tensor* lse, cea_tensor* final_out,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  CEA_REQUIRE(out && lse && final_out, CEA_EINVAL, "attention_merge_final: missing tensor");
+  AttnParams p;
+  int rc = make_attn_params(&p, q, k, v, q_pos, k_pos, causal, scale, kv_map, kv_map_len, out,
+                            lse, 1);
+  if (rc) return rc;
+  if ((rc = check_tensor(final_out, "final_out", 4, -1, true))) return rc;
+  CEA_REQUIRE(final_out->dtype == out->dtype || final_out->dtype == q->dtype, CEA_EINVAL,
+              "attention_merge_final: final_out must be %s or %s", dtype_name(out->dtype),
+              dtype_name(q->dtype));
+  for (int j = 0; j < 4; ++j)
+    CEA_REQUIRE(final_out->size[j] == out->size[j], CEA_EINVAL,
+                "attention_merge_final: final_out must be [B, Sq, Hq, D]");
+  hipStream_t st = (hipStream_t)stream;
+  p.final_out = final_out->data;
+  p.fs_b = final_out->stride[0];
+  p.fs_s = final_out->stride[1];
+  p.fs_h = final_out->stride[2];
+  p.final_dtype = final_out->dtype;
+  if (p.Sk > 0 && !use_decode(p) && prefill_mfma_supported(p))
+    return run_attention(p, (char*)workspace, workspace_bytes, st);
+  // other kernels: merge into the running pair, then cast it (a one-partial merge)
+  p.final_out = nullptr;
+  if (p.Sk > 0 && (rc = run_attention(p, (char*)workspace, workspace_bytes, st))) return rc;
+  return merge_impl(1, out, lse, final_out, nullptr, 0, st);
+}
+
 static int fill_merge_part(MergeParams* m, int i, const cea_tensor* o, const cea_tensor* l,
                            int64_t B, int64_t Sq, int64_t H, int64_t D, int dt) {
   int rc;

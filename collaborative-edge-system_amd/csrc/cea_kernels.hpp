@@ -31,6 +31,10 @@ struct AttnParams {
   int32_t out_dtype;
   int32_t ntiles;
   HeadMap map;
+  // accumulate only: the merged output goes here (in final_dtype) instead of into out
+  void* final_out;
+  int64_t fs_b, fs_s, fs_h;
+  int32_t final_dtype;
 };
 
 // n-way merge of partial results (n <= CEA_MAX_PARTS).

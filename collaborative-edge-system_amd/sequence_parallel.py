@@ -38,6 +38,7 @@ from .attention import (
     attention,
     attention_with_lse,
     attention_with_lse_into,
+    _merge_list,
     merge_attention_list,
     merge_packed,
     pack_partial,
@@ -111,10 +112,13 @@ def ring_attention(
     kv_block: Optional[int] = None,
 ) -> torch.Tensor:
     """Attention of this rank's queries over the KV blocks of all ranks
-    (sequence_parallel.py:68-130); returns ``[B, s_r, Hq, D]`` in ``q.dtype``."""
+    (sequence_parallel.py:68-130); returns ``[B, s_r, Hq, D]`` in ``q.dtype``.  The last
+    block's merge writes the result in ``q.dtype`` directly (the reference's final
+    ``out.to(q.dtype)``, :128, in the same kernel)."""
+    final = torch.empty(q.shape, dtype=q.dtype, device=q.device) if comm.size > 1 else None
     out, _ = ring_attention_with_lse(q, k, v, q_pos, k_pos, comm, kv_sizes, causal=causal,
-                                     scale=scale, kv_map=kv_map, kv_block=kv_block)
-    return out.to(q.dtype)
+                                     scale=scale, kv_map=kv_map, kv_block=kv_block, _final=final)
+    return final if final is not None else out.to(q.dtype)
 
 
 def ring_attention_with_lse(
@@ -130,8 +134,11 @@ def ring_attention_with_lse(
     scale: Optional[float] = None,
     kv_map: KVMap = None,
     kv_block: Optional[int] = None,
+    _final: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """:func:`ring_attention` returning the merged ``(out, lse)`` in accumulation precision."""
+    """:func:`ring_attention` returning the merged ``(out, lse)`` in accumulation precision
+    (``_final``: a tensor that receives the merged output of the last merge instead; ``out``
+    is then unspecified)."""
     n, r = comm.size, comm.rank
     if n == 1:
         return attention_with_lse(q, k, v, q_pos, k_pos, causal=causal, scale=scale,
@@ -144,7 +151,7 @@ def ring_attention_with_lse(
     out = torch.empty(B, Sq, Hq, D, dtype=acc, device=q.device)
     lse = torch.empty((B, Hq, Sq), dtype=acc, device=q.device)
     own = (k, v, k_pos)
-    first = True
+    launches = []
     for step in range(n):
         kb, vb, pb = _kv_from(comm, (r - step) % n, own)
         if kb.shape[1] != kv_sizes[(r - step) % n]:
@@ -152,13 +159,21 @@ def ring_attention_with_lse(
         blk = kv_block if kv_block is not None and kv_block < kb.shape[1] else kb.shape[1]
         for start in range(0, kb.shape[1], max(1, blk)):
             end = min(start + blk, kb.shape[1])
-            attention_with_lse_into(out, lse, q, kb[:, start:end], vb[:, start:end], q_pos,
-                                    pb[:, start:end], causal=causal, scale=scale, kv_map=kv_map,
-                                    accumulate=not first)
-            first = False
-    if first:  # no rank held a key: the merge's neutral element
+            launches.append((kb[:, start:end], vb[:, start:end], pb[:, start:end]))
+    if not launches:  # no rank held a key: the merge's neutral element
         out.zero_()
         lse.fill_(float("-inf"))
+        if _final is not None:
+            _final.zero_()
+        return out, lse
+    for i, (kb, vb, pb) in enumerate(launches):
+        last = i == len(launches) - 1
+        attention_with_lse_into(out, lse, q, kb, vb, q_pos, pb, causal=causal, scale=scale,
+                                kv_map=kv_map, accumulate=i > 0,
+                                final=_final if last and i > 0 else None)
+    if _final is not None and len(launches) == 1:  # a one-partial merge casts it
+        cast, _ = _merge_list([out], [lse], out_dtype=_final.dtype)
+        _final.copy_(cast)
     return out, lse
 
 

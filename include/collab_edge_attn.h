@@ -91,6 +91,22 @@ int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_t
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The last step of a ring: merges attention over one more KV block into the running
+ * (out, lse) exactly as cea_attention_with_lse with accumulate = 1, and writes the merged
+ * output to final_out (q's dtype or the accumulation dtype) instead of back into out.
+ * Replaces the last online merge of ring_attention together with its final
+ * `out.to(q.dtype)` (collab_infer/parallel/sequence_parallel.py:121, 128).
+ *   out, lse  the running pair (f32 / f64); lse receives the merged lse; out is read, and
+ *             its content after the call is unspecified
+ *   final_out [B,Sq,Hq,D]
+ */
+int cea_attention_merge_final(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
+                              const cea_tensor* q_pos, const cea_tensor* k_pos, int32_t causal,
+                              double scale, const int32_t* kv_map, int32_t kv_map_len,
+                              cea_tensor* out, cea_tensor* lse, cea_tensor* final_out,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Pairwise exact merge: lse = logaddexp(lse_a, lse_b); out = out_a*w_a + out_b*w_b.
  * Replaces merge_attention (collab_infer/parallel/attention.py:242-250).
  *   out_*  [B,Sq,H,D] f32/f64,  lse_* [B,H,Sq] same dtype.  out may alias out_a (each

@@ -160,3 +160,58 @@ def test_head_major_cache_views_and_kv_block(cea, dev, dtype):
     torch.cuda.synchronize()
     assert_attention_close(out, lse, ro, rl, dtype, "cache view")
     assert_attention_close(ob, lb, ro, rl, dtype, "cache view kv_block")
+
+
+@pytest.mark.parametrize("dtype,Sq,D,final_f32",
+                         [(torch.bfloat16, 300, 128, False), (torch.bfloat16, 300, 128, True),
+                          (torch.float16, 200, 64, False), (torch.float32, 40, 64, False),
+                          (torch.bfloat16, 1, 128, False), (torch.bfloat16, 100, 96, False)],
+                         ids=["bf16-mfma", "bf16-mfma-f32out", "f16-mfma", "f32-generic",
+                              "bf16-decode", "bf16-generic-d96"])
+def test_merge_final_equals_merge_then_cast(cea, dev, dtype, Sq, D, final_f32):
+    """The last ring merge with the cast fused (cea_attention_merge_final) returns exactly
+    merge-then-cast, on the MFMA kernel and on the kernels that fall back to a separate cast;
+    an empty block casts the running pair."""
+    g = torch.Generator().manual_seed(7)
+    B, Hq, Hkv, Sk = 2, 4, 2, 230
+    q = torch.randn(B, Sq, Hq, D, generator=g).to(dtype).to(dev)
+    k = torch.randn(B, Sk, Hkv, D, generator=g).to(dtype).to(dev)
+    v = torch.randn(B, Sk, Hkv, D, generator=g).to(dtype).to(dev)
+    qpos = (torch.arange(Sq) + 150).repeat(B, 1).to(dev)
+    kpos = torch.arange(Sk).repeat(B, 1)
+    kpos[1, 200:] = -1
+    kpos = kpos.to(dev)
+    out = torch.zeros(B, Sq, Hq, D, device=dev)
+    lse = torch.full((B, Hq, Sq), float("-inf"), device=dev)
+    cea.attention_with_lse_into(out, lse, q, k[:, :100], v[:, :100], qpos, kpos[:, :100])
+    out2, lse2 = out.clone(), lse.clone()
+    cea.attention_with_lse_into(out2, lse2, q, k[:, 100:], v[:, 100:], qpos, kpos[:, 100:])
+    fdt = torch.float32 if final_f32 else dtype
+    final = torch.empty(B, Sq, Hq, D, dtype=fdt, device=dev)
+    lse3 = lse.clone()
+    cea.attention_with_lse_into(out.clone(), lse3, q, k[:, 100:], v[:, 100:], qpos, kpos[:, 100:],
+                                final=final)
+    empty = torch.empty(B, Sq, Hq, D, dtype=fdt, device=dev)
+    lse4 = lse2.clone()
+    cea.attention_with_lse_into(out2.clone(), lse4, q, k[:, :0], v[:, :0], qpos, kpos[:, :0],
+                                final=empty)
+    torch.cuda.synchronize()
+    assert torch.equal(final, out2.to(fdt))
+    assert torch.equal(lse3, lse2)
+    assert torch.equal(empty, out2.to(fdt)) and torch.equal(lse4, lse2)
+
+
+def test_ring_attention_fused_cast_is_exact(cea, dev):
+    """ring_attention's last step writes the bf16 result in its epilogue: equal, bit for bit,
+    to the f32 merged output of ring_attention_with_lse cast to bf16, for the ring workload's
+    layout at reduced length (sp=4 zigzag, GQA 8/2, D=128)."""
+    w = cea.workloads.ring_share(device=dev, seq_len=4096, hq=8, hkv=2)
+    comm = cea.LocalGroup(w.layout.num_ranks, w.rank)
+    for r, (k, v, p) in enumerate(w.blocks):
+        comm.set_shard(r, k=k, v=v, pos=p)
+    k0, v0, p0 = w.blocks[w.rank]
+    res = cea.ring_attention(w.q, k0, v0, w.q_pos, p0, comm, w.kv_sizes)
+    o, _ = cea.sequence_parallel.ring_attention_with_lse(w.q, k0, v0, w.q_pos, p0, comm, w.kv_sizes)
+    torch.cuda.synchronize()
+    assert res.dtype == torch.bfloat16
+    assert torch.equal(res, o.to(torch.bfloat16))
