@@ -10,10 +10,12 @@ Import with ``importlib.import_module("collaborative-edge-system_amd")``.  Modul
 * :mod:`.kv_cache` - head-major KV cache with the rotary of K fused into the append
   (collab_infer/models/cache.py)
 * :mod:`.partition` - splits and sequence layouts (collab_infer/parallel/partition.py)
+* :mod:`.projection` - the fused Q/K/V and gate/up projection GEMM
+  (collab_infer/parallel/tensor_parallel.py:264-320)
 * :mod:`.workloads` - seeded inputs of the five measured workloads
 """
 
-from . import _native, attention, kv_cache, layers, partition, sequence_parallel, workloads  # noqa: F401
+from . import _native, attention, kv_cache, layers, partition, projection, sequence_parallel, workloads  # noqa: F401
 from .attention import (  # noqa: F401
     MASK_CHUNK_ELEMENTS,
     accumulation_dtype,
@@ -32,6 +34,7 @@ from .attention import (  # noqa: F401
 from .kv_cache import LayerKVCache, kv_append  # noqa: F401
 from .layers import RMSNorm, RotaryEmbedding, apply_rotary, rmsnorm, rmsnorm_rope, silu_mul  # noqa: F401
 from .partition import HeadShard, SequenceLayout, partition_heads, split_sizes  # noqa: F401
+from .projection import FusedColumnParallelLinear, fused_linear, linear  # noqa: F401
 from .sequence_parallel import (  # noqa: F401
     LocalGroup,
     distributed_kv_attention,

@@ -79,3 +79,9 @@ def rmsnorm_rope(x, weight, eps, positions, inv, num_heads):
 def silu_gate(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """llama.py:45, 305: F.silu(gate) * up."""
     return F.silu(gate) * up
+
+
+def linear(x, weight, bias=None):
+    """tensor_parallel.py:294-295: F.linear of the fused projection, in the input dtype on the
+    CPU (f32 accumulation for bf16 / f16 inputs)."""
+    return torch.nn.functional.linear(x, weight, bias)

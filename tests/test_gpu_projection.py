@@ -1,0 +1,97 @@
+"""GPU parity of the fused projection (``cea_linear``, hipBLASLt) against the oracle's
+``F.linear`` on the CPU (tensor_parallel.py:294-295).
+
+Tolerance: the GEMM accumulates in f32 in another order than the CPU, so each output may sit
+on the other side of one rounding step of the output dtype: |gpu - cpu| <= 1 ulp of the
+output dtype at |cpu| plus 1e-4 of max |cpu|, for every element (f32: 1e-5 normwise).
+"""
+
+import pytest
+import torch
+
+from oracle import layers_ref as L
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulp(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    mant = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23}[dtype]
+    e = torch.floor(torch.log2(x.abs().clamp(min=2.0 ** -24)))
+    return torch.pow(2.0, e - mant)
+
+
+def _check(got: torch.Tensor, want: torch.Tensor):
+    dtype = got.dtype
+    got, want = got.cpu().double(), want.double()
+    if dtype == torch.float32:
+        assert (got - want).abs().max().item() <= 1e-5 * want.abs().max().item()
+        return
+    err = (got - want).abs()
+    assert bool((err <= _ulp(want, dtype) + 1e-4 * want.abs().max()).all()), err.max().item()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=str)
+@pytest.mark.parametrize("N,K,M,bias", [(1, 64, 96, False), (37, 256, 384, True), (300, 1024, 640, False),
+                                        (513, 512, 1536, True), (64, 4096, 1, True)])
+def test_linear_matches_oracle(cea, dev, dtype, N, K, M, bias):
+    g = torch.Generator().manual_seed(N + K + M)
+    x = torch.randn(N, K, generator=g).to(dtype)
+    w = (torch.randn(M, K, generator=g) / K ** 0.5).to(dtype)
+    b = torch.randn(M, generator=g).to(dtype) if bias else None
+    got = cea.linear(x.to(dev), w.to(dev), b.to(dev) if bias else None)
+    want = L.linear(x.float(), w.float(), b.float() if bias else None).to(dtype)
+    torch.cuda.synchronize()
+    assert got.dtype == dtype and got.shape == (N, M)
+    if dtype == torch.float32:
+        want = L.linear(x.double(), w.double(), b.double() if bias else None)
+    _check(got, want)
+
+
+def test_fused_qkv_projection_views_feed_the_kernels(cea, dev):
+    """FusedColumnParallelLinear over Q/K/V of a 3-D input: the per-projection outputs are
+    column views of one GEMM (strided rows), equal to separate projections, and feed the
+    KV-cache append (rotary of K) and plain attention without copies."""
+    g = torch.Generator().manual_seed(1)
+    B, S, hidden, hq, hkv, d = 2, 70, 512, 8, 2, 64
+    layer = cea.FusedColumnParallelLinear(hidden, [(hq * d, 0, hq * d), (hkv * d, 0, hkv * d),
+                                                   (hkv * d, 0, hkv * d)], None, bias=True,
+                                          dtype=torch.bfloat16, device=dev)
+    ws = [(torch.randn(n, hidden, generator=g) / hidden ** 0.5).to(torch.bfloat16)
+          for n in (hq * d, hkv * d, hkv * d)]
+    bs = [torch.randn(n, generator=g).to(torch.bfloat16) for n in (hq * d, hkv * d, hkv * d)]
+    layer.load_full(ws, bs)
+    x = torch.randn(B, S, hidden, generator=g).to(torch.bfloat16)
+    q, k, v = layer(x.to(dev))
+    assert q.shape == (B, S, hq * d) and not k.is_contiguous()
+    for got, w, bb in zip((q, k, v), ws, bs):
+        _check(got, L.linear(x.float(), w.float(), bb.float()).to(torch.bfloat16))
+    # the views go into the kernels as they are
+    q4, k4, v4 = q.view(B, S, hq, d), k.view(B, S, hkv, d), v.view(B, S, hkv, d)
+    pos = torch.arange(S, device=dev).repeat(B, 1)
+    out = cea.attention_fn(q4, k4, v4, pos, pos)
+    ref = cea.attention_fn(q4.contiguous(), k4.contiguous(), v4.contiguous(), pos, pos)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+def test_linear_under_graph_capture(cea, dev):
+    """A shape first seen inside HIP-graph capture keeps the heuristic's first algorithm (no
+    timing inside the capture); every replay, with eager work between replays, matches the
+    oracle, and so does the eager call that follows (which then times the candidates)."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(96, 320, generator=g).to(torch.bfloat16).to(dev)
+    w = torch.randn(448, 320, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.empty(96, 448, dtype=torch.bfloat16, device=dev)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        cea.linear(x, w, out=out)
+    torch.cuda.synchronize()
+    want = cea.linear(x, w)
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        _check(out, L.linear(x.cpu().float(), w.cpu().float()).to(torch.bfloat16))
+    _check(want, L.linear(x.cpu().float(), w.cpu().float()).to(torch.bfloat16))

@@ -227,3 +227,33 @@ def test_rmsnorm_rope_f64_composition():
     normed = _rms_closed(x.numpy(), w.numpy(), 1e-5).reshape(S, H, D)
     want = _rope_complex(normed, pos.numpy(), inv.numpy())
     assert np.abs(y - want).max() <= 1e-12
+
+
+# ---- fused projection (tensor_parallel.py:294-295) -----------------------------------------
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |x| (2^(e-7) for |x| in [2^e, 2^(e+1)))."""
+    e = torch.floor(torch.log2(x.abs().clamp(min=2.0 ** -126)))
+    return torch.pow(2.0, e - 7)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_oracle_linear_closed_form(bias):
+    """The oracle's projection equals x . W^T + b computed in f64, to the output rounding (bf16:
+    within one bf16 ulp of the f64 value plus the f32 accumulation error); a transposed
+    weight or a dropped bias is rejected by the same check."""
+    g = torch.Generator().manual_seed(3)
+    N, K, M = 37, 256, 256
+    x = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(M, K, generator=g) / 16).to(torch.bfloat16)
+    b = torch.randn(M, generator=g).to(torch.bfloat16) if bias else None
+    exact = x.double() @ w.double().T + (b.double() if bias else 0)
+
+    def close(y):
+        err = (y.double() - exact).abs()
+        return bool((err <= _bf16_ulp(exact) + 1e-4 * exact.abs().max()).all())
+
+    assert close(L.linear(x, w, b))
+    assert not close(L.linear(x, w.T.contiguous(), b))
+    if bias:
+        assert not close(L.linear(x, w, None))
