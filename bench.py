@@ -61,7 +61,7 @@ def _timed(fn, steps: int, warmup: int, torch):
 def _graph_timed(fn, steps: int, warmup: int, torch, per_graph: int = 20):
     """Seconds per call of ``fn`` from replays of a HIP graph holding ``per_graph`` calls:
     the GPU time of a launch, without the host's per-call launch cost (which exceeds the
-    kernel time of the small layer ops)."""
+    kernel time of the small layer ops); the median of 5 timed runs."""
     fn()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -72,12 +72,15 @@ def _graph_timed(fn, steps: int, warmup: int, torch, per_graph: int = 20):
         g.replay()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(steps):
-        g.replay()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) * 1e-3 / (steps * per_graph)
+    times = []
+    for _ in range(5):  # median of 5 timed runs of `steps` replays each
+        a.record()
+        for _ in range(steps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) * 1e-3 / (steps * per_graph))
+    return sorted(times)[2]
 
 
 def bench_ring(cea, torch, steps, warmup, dev):

@@ -388,6 +388,18 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(
 // stores beat every other combination for this read-once, write-once row pass).  The position and frequency loads of the
 // rotary table entries are issued ahead of the row loads (loads complete in order), so
 // the table evaluation overlaps the row loads instead of waiting behind them.
+// ---- bf16 pairs for the fused row kernel: one v_cvt_pk_bf16_f32 rounds two f32 values to
+// bf16 (nearest even); the low half widens back with a shift, the high half with a mask
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  return u;
+}
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
 template <typename T, int VEC, int R>
 __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
     const T* __restrict__ x, int64_t xs, const T* __restrict__ w, const int64_t* __restrict__ pos,
@@ -397,8 +409,9 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
   static_assert(VEC * sizeof(T) == 16, "16-byte chunks");
   constexpr int TE = (R * 256 + 255) / 256;  // table entries per thread (half <= 256)
   __shared__ M red[R][4];
-  __shared__ T tab_c[R][256];
-  __shared__ T tab_s[R][256];
+  // the tables hold the T-rounded cos / sin widened back to M, ready for the products
+  __shared__ __attribute__((aligned(16))) M tab_c[R][256];
+  __shared__ __attribute__((aligned(16))) M tab_s[R][256];
   const int64_t row0 = (int64_t)blockIdx.x * R;
   const int C = H * D;
   const int half = D / 2;
@@ -442,8 +455,8 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
     if (t < R * half) {
       M sv, cv;
       sincos_acc(ang[k], &sv, &cv);
-      tab_c[r][jj] = narrow<T, M>(cv);
-      tab_s[r][jj] = narrow<T, M>(sv);
+      tab_c[r][jj] = rnd<T, M>(cv);
+      tab_s[r][jj] = rnd<T, M>(sv);
     }
   }
 #pragma unroll
@@ -460,6 +473,56 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
   }
   __syncthreads();  // publishes the partial sums and the tables
   if (!active) return;
+  if constexpr (__is_same(T, bf16)) {
+    // the same rounding points on pairs: every rounding of two values is one conversion
+    constexpr int NP = VEC / 2;
+    uint32_t wp1[NP], wp2[NP];
+    __builtin_memcpy(wp1, w1, 16);
+    __builtin_memcpy(wp2, w2, 16);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (row0 + r >= S) break;
+      const M ss = red[r][0] + red[r][1] + red[r][2] + red[r][3];
+      const float rs = rsqrt_rn(add_rn(div_rn(ss, (M)C), (M)eps_d));
+      uint32_t xp1[NP], xp2[NP], o1[NP], o2[NP];
+      __builtin_memcpy(xp1, x1[r], 16);
+      __builtin_memcpy(xp2, x2[r], 16);
+      float cf[VEC], sf[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; e += 4) {
+        *(float4*)&cf[e] = *(const float4*)&tab_c[r][j + e];
+        *(float4*)&sf[e] = *(const float4*)&tab_s[r][j + e];
+      }
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        // RMSNorm: yn = (x * rs).to(bf16); y = (w * yn).to(bf16)
+        const uint32_t yn1 = pack_bf16(mul_rn(bf16_lo(xp1[q]), rs), mul_rn(bf16_hi(xp1[q]), rs));
+        const uint32_t yn2 = pack_bf16(mul_rn(bf16_lo(xp2[q]), rs), mul_rn(bf16_hi(xp2[q]), rs));
+        const uint32_t y1 = pack_bf16(mul_rn(bf16_lo(wp1[q]), bf16_lo(yn1)), mul_rn(bf16_hi(wp1[q]), bf16_hi(yn1)));
+        const uint32_t y2 = pack_bf16(mul_rn(bf16_lo(wp2[q]), bf16_lo(yn2)), mul_rn(bf16_hi(wp2[q]), bf16_hi(yn2)));
+        const float a1[2] = {bf16_lo(y1), bf16_hi(y1)}, a2[2] = {bf16_lo(y2), bf16_hi(y2)};
+        float r1[2], r2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const float cv = cf[2 * q + u], sv = sf[2 * q + u];
+          // first half: (y1*cos).to(bf16) + (-y2*sin).to(bf16); second: y2*cos + y1*sin
+          const uint32_t pq1 = pack_bf16(mul_rn(a1[u], cv), mul_rn(a2[u], sv));
+          const uint32_t pq2 = pack_bf16(mul_rn(a2[u], cv), mul_rn(a1[u], sv));
+          r1[u] = add_rn(bf16_lo(pq1), -bf16_hi(pq1));
+          r2[u] = add_rn(bf16_lo(pq2), bf16_hi(pq2));
+        }
+        o1[q] = pack_bf16(r1[0], r1[1]);
+        o2[q] = pack_bf16(r2[0], r2[1]);
+      }
+      T v1[VEC], v2[VEC];
+      __builtin_memcpy(v1, o1, 16);
+      __builtin_memcpy(v2, o2, 16);
+      T* orow = out + (row0 + r) * os;
+      store_vec_stream<T, VEC>(orow + c1, v1);
+      store_vec_stream<T, VEC>(orow + c2, v2);
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (row0 + r >= S) break;
@@ -470,8 +533,8 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
     for (int e = 0; e < VEC; ++e) {
       y1[e] = narrow<T, M>(mul_rn(widen<T, M>(w1[e]), rnd<T, M>(mul_rn(widen<T, M>(x1[r][e]), rs))));
       y2[e] = narrow<T, M>(mul_rn(widen<T, M>(w2[e]), rnd<T, M>(mul_rn(widen<T, M>(x2[r][e]), rs))));
-      cs[e] = tab_c[r][j + e];
-      sn[e] = tab_s[r][j + e];
+      cs[e] = narrow<T, M>(tab_c[r][j + e]);
+      sn[e] = narrow<T, M>(tab_s[r][j + e]);
     }
     rotate_pair<T, M, VEC>(y1, y2, cs, cs, sn, sn, o1, o2);
     T* orow = out + (row0 + r) * os;
