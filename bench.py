@@ -237,28 +237,6 @@ def bench_wire(cea, torch, steps, warmup, dev):
     return res
 
 
-def bench_projection(cea, torch, steps, warmup, dev):
-    """The fused projections that feed the path, at the layer-op workload's model shape
-    (4096 tokens, hidden 4096, 32/8 heads of 128, intermediate 14336, bf16): the Q/K/V GEMM
-    [4096 x 4096] x [6144 x 4096]^T and the gate/up GEMM [4096 x 4096] x [28672 x 4096]^T
-    (hipBLASLt through cea_linear)."""
-    g = torch.Generator(device=dev).manual_seed(0)
-    x = torch.randn(4096, 4096, generator=g, device=dev).to(torch.bfloat16)
-    res = {}
-    for name, m in (("qkv", 32 * 128 + 2 * 8 * 128), ("gate_up", 2 * 14336)):
-        w = (torch.randn(m, 4096, generator=g, device=dev) / 64).to(torch.bfloat16)
-        out = torch.empty(4096, m, dtype=torch.bfloat16, device=dev)
-        sec = _timed(lambda: cea.linear(x, w, out=out), steps, warmup, torch)
-        flop = 2 * 4096 * 4096 * m
-        tf = flop / sec / 1e12
-        res[name] = {"value": round(tf, 1), "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-                     "ms_per_step": round(sec * 1e3, 4), "flop": flop}
-        del w, out
-    res["workload"] = ("fused projections of a 4096-token, hidden-4096 bf16 layer: Q/K/V "
-                       "(6144 outputs) and gate/up (2 x 14336 outputs), f32 accumulation")
-    return res
-
-
 def bench_ulysses(cea, torch, steps, warmup, dev):
     w = cea.workloads.ulysses_share(device=dev)
 
@@ -325,7 +303,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,kvappend,ulysses,wire,projection,f32")
+    ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,kvappend,ulysses,wire,f32")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a device copy of MIB MiB (HBM counter calibration) and exit")
@@ -368,9 +346,6 @@ def main() -> int:
     if want("ulysses"):
         _log("ulysses share")
         secondary["ulysses_share"] = bench_ulysses(cea, torch, max(5, args.steps // 2), args.warmup, dev)
-    if want("projection"):
-        _log("fused projections (hipBLASLt)")
-        secondary["projection"] = bench_projection(cea, torch, args.steps, args.warmup, dev)
     if want("wire"):
         _log("wire formats (Ulysses all-to-alls, packed distributed-KV merge)")
         secondary["wire"] = bench_wire(cea, torch, args.steps, args.warmup, dev)

@@ -10,7 +10,7 @@ Import with ``importlib.import_module("collaborative-edge-system_amd")``.  Modul
 * :mod:`.kv_cache` - head-major KV cache with the rotary of K fused into the append
   (collab_infer/models/cache.py)
 * :mod:`.partition` - splits and sequence layouts (collab_infer/parallel/partition.py)
-* :mod:`.projection` - the fused Q/K/V and gate/up projection GEMM
+* :mod:`.projection` - the fused Q/K/V and gate/up projections (torch's GEMM, column views)
   (collab_infer/parallel/tensor_parallel.py:264-320)
 * :mod:`.workloads` - seeded inputs of the five measured workloads
 """

@@ -91,8 +91,6 @@ _SIGNATURES = {
         [_P, _P, ctypes.c_double, _P, _P, ctypes.c_int32, _P, ctypes.c_void_p],
     ),
     "cea_silu_mul": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p]),
-    "cea_linear_workspace_bytes": (ctypes.c_size_t, []),
-    "cea_linear": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "cea_kv_append": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int64, ctypes.c_void_p],

@@ -77,9 +77,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile, sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    # hipBLASLt runs the fused projection GEMM (csrc/linear.hip)
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           "-lhipblaslt"]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")

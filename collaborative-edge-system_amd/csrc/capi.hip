@@ -826,36 +826,6 @@ int cea_rmsnorm_rope(const cea_tensor* x, const cea_tensor* weight, double eps,
                              (hipStream_t)stream);
 }
 
-size_t cea_linear_workspace_bytes(void) { return (size_t)32 << 20; }
-
-int cea_linear(const cea_tensor* x, const cea_tensor* weight, const cea_tensor* bias,
-               cea_tensor* out, void* workspace, size_t workspace_bytes, void* stream) {
-  int rc;
-  if ((rc = check_tensor(x, "x", 2, -1, true))) return rc;
-  const int dt = x->dtype;
-  CEA_REQUIRE(dt == CEA_BF16 || dt == CEA_F16 || dt == CEA_F32, CEA_EUNSUPPORTED,
-              "linear: unsupported dtype %s", dtype_name(dt));
-  if ((rc = check_tensor(weight, "weight", 2, dt, true))) return rc;
-  if ((rc = check_tensor(out, "out", 2, dt, true))) return rc;
-  const int64_t N = x->size[0], K = x->size[1], M = weight->size[0];
-  CEA_REQUIRE(weight->size[1] == K, CEA_EINVAL, "linear: weight must be [M, %lld]", (long long)K);
-  CEA_REQUIRE(out->size[0] == N && out->size[1] == M, CEA_EINVAL, "linear: out must be [N, M]");
-  CEA_REQUIRE(K >= 1, CEA_EUNSUPPORTED, "linear: empty reduction dimension");
-  if (bias) {
-    if ((rc = check_tensor(bias, "bias", 1, dt, true))) return rc;
-    CEA_REQUIRE(bias->size[0] == M, CEA_EINVAL, "linear: bias must be [M]");
-  }
-  // leading dimensions of the column-major view (a single row may carry any stride)
-  cea_tensor xx = *x, ww = *weight, oo = *out;
-  if (N == 1 && xx.stride[0] < K) xx.stride[0] = K;
-  if (M == 1 && ww.stride[0] < K) ww.stride[0] = K;
-  if (N == 1 && oo.stride[0] < M) oo.stride[0] = M;
-  CEA_REQUIRE(xx.stride[0] >= K && ww.stride[0] >= K && oo.stride[0] >= M, CEA_EINVAL,
-              "linear: rows of x, weight and out must not overlap");
-  CEA_REQUIRE(workspace != nullptr || workspace_bytes == 0, CEA_EINVAL, "linear: null workspace");
-  return launch_linear(&xx, &ww, bias, &oo, workspace, workspace_bytes, (hipStream_t)stream);
-}
-
 int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, void* stream) {
   int rc;
   if ((rc = check_tensor(gate, "gate", 2, -1, true))) return rc;

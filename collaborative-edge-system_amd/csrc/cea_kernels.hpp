@@ -137,8 +137,6 @@ struct UlyssesGatherParams {
 };
 
 int launch_merge(const MergeParams& p, hipStream_t s);
-int launch_linear(const cea_tensor* x, const cea_tensor* w, const cea_tensor* bias,
-                  cea_tensor* out, void* workspace, size_t ws_bytes, hipStream_t st);
 int launch_pack_partial(const PackParams& p, hipStream_t s);
 int launch_ulysses_scatter(const UlyssesScatterParams& p, int vec, hipStream_t s);
 int launch_ulysses_gather(const UlyssesGatherParams& p, int vec, hipStream_t s);

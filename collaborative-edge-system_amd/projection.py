@@ -1,54 +1,45 @@
 """The fused Q/K/V and gate/up projections that feed the attention and layer-op kernels,
 drop-in for collab_infer/parallel/tensor_parallel.py:264-320 (``FusedColumnParallelLinear``).
 
-* :func:`linear` - ``F.linear(x, weight, bias)`` through ``cea_linear`` (hipBLASLt, f32
-  accumulation, bias added before the one rounding to the output dtype)
+The projection itself is a plain library GEMM: it stays the reference's ``F.linear``, run by
+PyTorch's own BLAS on the device (this package ships no GEMM kernel and links no BLAS
+library of its own, so it never mixes a second BLAS build into the process).  What this
+module adds is the layout contract: the per-projection outputs are column views of the one
+GEMM output, and the rotary, KV-cache append, SiLU-gate and attention kernels take those
+strided rows as they are, without a copy.
+
+* :func:`linear` - ``F.linear(x, weight, bias)`` for device tensors
 * :func:`fused_linear` - the same, returned as the per-projection column views of
-  ``.split(local_sizes, dim=-1)``; the views go straight into the rotary, KV-cache append
-  and SiLU-gate kernels, which take strided rows
+  ``.split(local_sizes, dim=-1)``
 * :class:`FusedColumnParallelLinear` - the reference module on one device (its ``comm`` is
   kept for the signature; the local weight is the concatenation of the local slices)
 """
 
 from __future__ import annotations
 
-from ctypes import byref
 from typing import List, Optional, Sequence, Tuple
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import _native as nat
-from .attention import _inner_contiguous
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
            out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``F.linear(x, weight, bias)`` for ``x [..., K]``, ``weight [M, K]``, ``bias [M]``;
-    returns ``[..., M]`` in x's dtype (``out`` may be a preallocated ``[N, M]`` buffer with
-    free row stride, N = product of x's leading sizes)."""
+    """``F.linear(x, weight, bias)`` for ``x [..., K]``, ``weight [M, K]``, ``bias [M]`` on the
+    device; ``out`` may be a preallocated ``[N, M]`` buffer (N = product of x's leading sizes)."""
     nat.require_device(x, weight, bias, out)
     if weight.dim() != 2 or x.shape[-1] != weight.shape[1]:
         raise ValueError(f"linear: x [..., {x.shape[-1]}] does not match weight {tuple(weight.shape)}")
     if weight.dtype != x.dtype or (bias is not None and bias.dtype != x.dtype):
         raise ValueError("linear: x, weight and bias must share a dtype")
-    lead = x.shape[:-1]
-    K, M = x.shape[-1], weight.shape[0]
-    x2 = _inner_contiguous(x.reshape(-1, K))
-    weight = _inner_contiguous(weight)
-    if bias is not None:
-        bias = bias.contiguous()
-    res = out if out is not None else torch.empty(x2.shape[0], M, dtype=x.dtype, device=x.device)
-    lib = nat.load_library()
-    nbytes = lib.cea_linear_workspace_bytes()
-    ws = nat.workspace(nbytes, x.device)
-    a = [nat.tensor_arg(t) for t in (x2, weight)]
-    b = nat.tensor_arg(bias) if bias is not None else None
-    o = nat.tensor_arg(res)
-    rc = lib.cea_linear(byref(a[0]), byref(a[1]), byref(b) if b is not None else None, byref(o),
-                        ws.data_ptr(), ws.numel(), nat.stream_of(x.device))
-    nat.check(rc, "linear")
-    return res if out is not None else res.view(*lead, M)
+    y = F.linear(x, weight, bias)
+    if out is None:
+        return y
+    out.copy_(y.reshape(-1, weight.shape[0]))
+    return out
 
 
 def fused_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],

@@ -260,20 +260,6 @@ int cea_rmsnorm_rope(const cea_tensor* x, const cea_tensor* weight, double eps,
  */
 int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, void* stream);
 
-/*
- * Fused column-parallel projection: out = x . weight^T (+ bias), f32 accumulation, the bias
- * added before the one rounding to the output dtype (hipBLASLt).
- * Replaces F.linear(x, self.weight, self.bias) of FusedColumnParallelLinear.forward
- * (collab_infer/parallel/tensor_parallel.py:294-295), the single GEMM behind the Q/K/V and
- * gate/up projections; its .split(local_sizes, dim=-1) are column views of out.
- *   x [N,K], weight [M,K], bias [M] or NULL, out [N,M], all bf16 / f16 / f32, innermost
- *   stride 1, row strides free; workspace of cea_linear_workspace_bytes() bytes (or fewer:
- *   the library then picks among algorithms that fit).
- */
-size_t cea_linear_workspace_bytes(void);
-int cea_linear(const cea_tensor* x, const cea_tensor* weight, const cea_tensor* bias,
-               cea_tensor* out, void* workspace, size_t workspace_bytes, void* stream);
-
 #ifdef __cplusplus
 }
 #endif
