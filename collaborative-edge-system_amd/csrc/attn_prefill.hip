@@ -436,6 +436,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
                          : nullptr;
   if (p.accumulate) {
     const float lse_old = *lse_ptr;
+    // a row that sees no key of this block merges to exactly its running pair (weights 1
+    // and 0); only a final output still has to be written
+    if (empty && !p.final_out && lse_old > -__builtin_inff()) return;
     const float lse = logaddexp<float>(lse_old, lse_new);
     const float safe = is_finite(lse) ? lse : 0.f;
     const float w_old = expf(lse_old - safe), w_new = expf(lse_new - safe);
