@@ -53,9 +53,11 @@ class LocalGroup:
 
     It stands in for collab_infer's ``Communicator`` (distributed/comm.py:200): instead of
     exchanging messages, every rank's shard is registered up front with :meth:`set_shard`
-    (keys ``k``, ``v``, ``pos`` for KV blocks; ``q`` too for Ulysses).  ``wire_dtype``
-    mirrors the ring's wire compression (``Communicator.to_wire``, comm.py:275-290): blocks
-    received from other ranks are rounded through that dtype.
+    (keys ``k``, ``v``, ``pos`` for KV blocks; ``q`` too for Ulysses).  ``wire_dtype`` is the
+    communicator's activation wire dtype (``comm_dtype``, distributed/comm.py:259-262) with
+    its rules (comm.py:275-290): a floating tensor travels in it only when it is narrower
+    than the tensor's own dtype, and float16 saturates at +-65504 instead of overflowing.
+    Pieces that cross the wire are rounded through it on arrival.
     """
 
     def __init__(self, size: int, rank: int = 0, wire_dtype: Optional[torch.dtype] = None) -> None:
@@ -81,10 +83,27 @@ class LocalGroup:
         g._shards = self._shards
         return g
 
-    def received(self, t: torch.Tensor) -> torch.Tensor:
-        if self.wire_dtype is None or self.wire_dtype == t.dtype:
+    def wire_dtype_for(self, dtype: torch.dtype) -> torch.dtype:
+        """The dtype ``dtype`` travels in (Communicator.wire_dtype, comm.py:284-290)."""
+        wire = self.wire_dtype
+        if wire is None or not dtype.is_floating_point:
+            return dtype
+        itemsize = torch.empty(0, dtype=dtype).element_size()
+        return wire if torch.empty(0, dtype=wire).element_size() < itemsize else dtype
+
+    def to_wire(self, t: torch.Tensor) -> torch.Tensor:
+        """``t`` in its wire dtype (Communicator.to_wire, comm.py:275-282)."""
+        wire = self.wire_dtype_for(t.dtype)
+        if wire == t.dtype:
             return t
-        return t.to(self.wire_dtype).to(t.dtype)
+        if wire == torch.float16:
+            t = t.clamp(-65504.0, 65504.0)
+        return t.to(wire)
+
+    def received(self, t: torch.Tensor) -> torch.Tensor:
+        """``t`` as it arrives after a compressed transfer (sent in the wire dtype, cast back)."""
+        w = self.to_wire(t)
+        return t if w is t else w.to(t.dtype)
 
 
 def _kv_from(comm: LocalGroup, src: int, own: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]):
@@ -337,8 +356,8 @@ def ulysses_scatter(q, k, v, positions, comm: LocalGroup, seq_sizes: Sequence[in
             sq, sk, sv, sp = s["q"], s["k"], s["v"], s["pos"]
             if sq.shape[1] != seq_sizes[j]:
                 raise ValueError(f"seq_sizes {list(seq_sizes)} inconsistent with rank {j}")
-        if comm.wire_dtype is not None and n > 1:
-            sq, sk, sv = (x.to(comm.wire_dtype).to(x.dtype) for x in (sq, sk, sv))
+        if n > 1:
+            sq, sk, sv = (comm.received(x) for x in (sq, sk, sv))
         shards.append((_heads_contiguous(sq), _heads_contiguous(sk), _heads_contiguous(sv),
                        _positions(sp)))
     nat.require_device(*[t for sh in shards for t in sh])
@@ -366,8 +385,8 @@ def ulysses_gather(out_heads_of_ranks: Sequence[torch.Tensor], comm: LocalGroup,
     outs = list(out_heads_of_ranks)
     if len(outs) != comm.size:
         raise ValueError("need one head output per rank")
-    if comm.wire_dtype is not None and comm.size > 1:
-        outs = [o.to(comm.wire_dtype).to(o.dtype) for o in outs]
+    if comm.size > 1:
+        outs = [comm.received(o) for o in outs]
     outs = [_heads_contiguous(o) for o in outs]
     nat.require_device(*outs)
     start = offsets_of(seq_sizes)[r]

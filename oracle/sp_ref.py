@@ -94,3 +94,15 @@ def ulysses_gather(out_heads, seq_sizes: Sequence[int], rank: int):
 def ulysses_local(q_f, k_f, v_f, pos_f, kv_map=None, *, causal=True, scale=None):
     """sequence_parallel.py:237: the head-sharded local attention after the scatter."""
     return plain_attention(q_f, k_f, v_f, pos_f, pos_f, causal=causal, scale=scale, kv_map=kv_map)
+
+
+def wire_round(t: torch.Tensor, activation_dtype) -> torch.Tensor:
+    """A tensor after a compressed transfer (distributed/comm.py:275-290, 468-486): floating
+    tensors travel in ``activation_dtype`` only when it is narrower than their own dtype,
+    float16 saturating at +-65504 (to_wire), and are cast back on arrival."""
+    if activation_dtype is None or not t.dtype.is_floating_point:
+        return t
+    if torch.empty(0, dtype=activation_dtype).element_size() >= t.element_size():
+        return t
+    w = t.clamp(-65504.0, 65504.0) if activation_dtype == torch.float16 else t
+    return w.to(activation_dtype).to(t.dtype)

@@ -291,3 +291,49 @@ def test_wire_pins_reject_planted_mistakes():
         parts.append(torch.cat([o, l.reshape(B, S, HQ, 1)], dim=-1))
     merged = sp_ref.merge_packed(parts, torch.float64)
     assert (merged - full)[pos >= 0].abs().max().item() > 1e-3
+
+
+# ---- wire compression rules (comm.py:275-290) ------------------------------------------------
+
+def _wire_pin(round_fn) -> bool:
+    """Closed forms of the compressed transfer: saturation of float16, bf16 rounding of f32/f64,
+    no compression into a dtype of the same width, integers untouched."""
+    x = torch.tensor([1e6, -1e6, 70000.0, 65519.0, 1.0, 2.0e-8, 1.0 + 2.0 ** -12])
+    ok = torch.equal(round_fn(x, torch.float16),
+                     torch.tensor([65504.0, -65504.0, 65504.0, 65504.0, 1.0, 0.0, 1.0]))
+    ok &= torch.equal(round_fn(x, torch.bfloat16), x.to(torch.bfloat16).to(torch.float32))
+    ok &= torch.equal(round_fn(x.double(), torch.bfloat16), x.double().to(torch.bfloat16).double())
+    xb = torch.tensor([1e20, 1.0 + 2.0 ** -7, -3.0], dtype=torch.bfloat16)
+    ok &= torch.equal(round_fn(xb, torch.float16), xb)  # same width: sent as it is
+    xh = torch.tensor([60000.0, 1.0 + 2.0 ** -10], dtype=torch.float16)
+    ok &= torch.equal(round_fn(xh, torch.bfloat16), xh)
+    pos = torch.tensor([0, 5, -1])
+    ok &= torch.equal(round_fn(pos, torch.float16), pos)
+    ok &= torch.equal(round_fn(x, None), x)
+    return bool(ok)
+
+
+def test_wire_rounding_pins():
+    assert _wire_pin(sp_ref.wire_round)
+
+
+def test_local_group_wire_rules_match_the_oracle():
+    def via_group(t, wire):
+        return cea.LocalGroup(2, 0, wire_dtype=wire).received(t)
+    assert _wire_pin(via_group)
+
+
+def test_wire_pin_rejects_planted_mistakes():
+    def no_clamp(t, wire):  # float16 overflows to inf
+        if wire is None or not t.dtype.is_floating_point or wire == t.dtype:
+            return t
+        return t.to(wire).to(t.dtype)
+
+    def always(t, wire):  # compresses into a dtype of the same width
+        if wire is None or not t.dtype.is_floating_point:
+            return t
+        w = t.clamp(-65504.0, 65504.0) if wire == torch.float16 else t
+        return w.to(wire).to(t.dtype)
+
+    assert not _wire_pin(no_clamp)
+    assert not _wire_pin(always)
