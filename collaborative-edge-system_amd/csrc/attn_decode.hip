@@ -555,15 +555,9 @@ int launch_nr(const DecodeParams& p, hipStream_t st) {
   if (total > 0) {
     hipLaunchKernelGGL(decode_vis_kernel, dim3(total, p.B), dim3(DTHREADS), 0, st, p);
     CEA_CHECK_LAUNCH("decode_vis");
-    static bool configured = false;
-    if (!configured) {
-      hipError_t e = hipFuncSetAttribute((const void*)decode_split_kernel<T, D, NR>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         DLayout<D>::LDS_BYTES);
-      CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "decode: cannot reserve %d bytes of LDS: %s",
-                  DLayout<D>::LDS_BYTES, hipGetErrorString(e));
-      configured = true;
-    }
+    const hipError_t e = reserve_lds<decode_split_kernel<T, D, NR>>(DLayout<D>::LDS_BYTES);
+    CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "decode: cannot reserve %d bytes of LDS: %s",
+                DLayout<D>::LDS_BYTES, hipGetErrorString(e));
     hipLaunchKernelGGL((decode_split_kernel<T, D, NR>), dim3(total, p.Hkv, p.B), dim3(DTHREADS),
                        DLayout<D>::LDS_BYTES, st, p);
     CEA_CHECK_LAUNCH("decode_split");

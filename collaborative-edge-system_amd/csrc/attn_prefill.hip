@@ -509,15 +509,9 @@ int launch_typed(const AttnParams& p, hipStream_t st) {
   const int64_t total = (int64_t)nqb * p.Hq * p.B;
   if (total == 0) return CEA_OK;
   CEA_REQUIRE(total < (int64_t)1 << 31, CEA_EUNSUPPORTED, "attention: grid too large");
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute((const void*)attn_prefill_kernel<T, D>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       Layout<D>::LDS_BYTES);
-    CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "attention: cannot reserve %d bytes of LDS: %s",
-                Layout<D>::LDS_BYTES, hipGetErrorString(e));
-    configured = true;
-  }
+  const hipError_t e = reserve_lds<attn_prefill_kernel<T, D>>(Layout<D>::LDS_BYTES);
+  CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "attention: cannot reserve %d bytes of LDS: %s",
+              Layout<D>::LDS_BYTES, hipGetErrorString(e));
   hipLaunchKernelGGL((attn_prefill_kernel<T, D>), dim3((unsigned)total), dim3(NTHREADS),
                      Layout<D>::LDS_BYTES, st, p);
   CEA_CHECK_LAUNCH("attention_prefill");

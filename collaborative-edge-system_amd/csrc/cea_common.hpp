@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
+#include <atomic>
 #include <string>
 
 #include "collab_edge_attn.h"
@@ -36,6 +37,22 @@ const char* last_error();
       return CEA_ELAUNCH;                                                         \
     }                                                                             \
   } while (0)
+
+// Raises a kernel's dynamic LDS limit to 'bytes' on the current device, once per device
+// (kernel attributes are per device; the first call on a device does the work, concurrent
+// first calls may both set it, which is harmless).
+template <auto Kernel>
+hipError_t reserve_lds(int bytes) {
+  static std::atomic<uint64_t> done{0};  // bit d: device d configured (devices 0..63)
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute((const void*)Kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
 
 inline size_t dtype_size(int32_t dt) {
   switch (dt) {
