@@ -82,6 +82,43 @@ def test_ring_share_bf16_matches_oracle(cea, dev):
     assert_attention_close(out, lse, ro, rl, torch.bfloat16, "ring share")
 
 
+@pytest.mark.parametrize("wire", [torch.bfloat16, torch.float16], ids=["bf16-wire", "f16-wire"])
+def test_ring_share_with_wire_compression(cea, dev, wire):
+    """f32 activations, compressed ring traffic (sequence_parallel.py:101-127, comm.py:275-290):
+    blocks from other ranks arrive rounded through the wire dtype (float16 saturating at
+    65504), the rank's own block stays at full precision.  Some keys and values exceed the
+    float16 range, so the saturation shows in the result."""
+    world, rank, S, hq, hkv, d = 4, 2, 256, 4, 2, 64
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, S, hq, d, generator=g) * 0.05
+    k = torch.randn(1, S, hkv, d, generator=g)
+    v = torch.randn(1, S, hkv, d, generator=g)
+    k[0, ::17, :, 3] = 9.0e4
+    v[0, ::13, :, 5] = -1.0e5
+    pos = torch.arange(S).repeat(1, 1)
+    layout = cea.SequenceLayout(S, world, None, "zigzag")
+    shards = [tuple(layout.shard(t, r) for t in (k, v, pos)) for r in range(world)]
+    group = cea.LocalGroup(world, rank, wire_dtype=wire)
+    for r, (kr, vr, pr) in enumerate(shards):
+        group.set_shard(r, k=kr.to(dev), v=vr.to(dev), pos=pr.to(dev))
+    qr, qp = layout.shard(q, rank), layout.shard(pos, rank)
+    own = shards[rank]
+    out, lse = cea.sequence_parallel.ring_attention_with_lse(
+        qr.to(dev), own[0].to(dev), own[1].to(dev), qp.to(dev), own[2].to(dev), group,
+        layout.sizes)
+    blocks = [(kr, vr, pr) if r == rank else
+              (sp_ref.wire_round(kr, wire), sp_ref.wire_round(vr, wire), pr)
+              for r, (kr, vr, pr) in enumerate(shards)]
+    ro, rl = sp_ref.ring_share(qr, qp, blocks, rank, with_lse=True)
+    torch.cuda.synchronize()
+    assert_attention_close(out, lse, ro, rl, torch.float32, f"ring share, {wire} wire")
+    if wire == torch.float16:  # the unsaturated transfer would differ
+        inf_blocks = [(kr, vr, pr) if r == rank else (kr.half().float(), vr.half().float(), pr)
+                      for r, (kr, vr, pr) in enumerate(shards)]
+        bad, _ = sp_ref.ring_share(qr, qp, inf_blocks, rank, with_lse=True)
+        assert not torch.allclose(bad, ro, equal_nan=True)
+
+
 DECODE_CASES = [
     # (B, Sq, Hq, Hkv, cap, parts)
     (3, 1, 32, 8, 700, [400, 300]),
