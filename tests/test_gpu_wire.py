@@ -97,6 +97,37 @@ def test_ulysses_scatter_strided_views_and_wire_rounding(cea, dev):
             assert torch.equal(a.cpu(), b_)
 
 
+def test_ulysses_wire_compression_rules(cea, dev):
+    """float16 wire: f32 pieces saturate at 65504 on the way (comm.py:275-282), the positions
+    are never compressed, and bf16 activations do not go through an f16 wire at all (same
+    width, comm.py:284-290)."""
+    world, hq, hkv, D, B, S = 2, 4, 2, 32, 1, 40
+    g = torch.Generator().manual_seed(9)
+    heads = cea.partition_heads(hq, hkv, world)
+    layout = cea.SequenceLayout(S, world, None, "contiguous")
+    pos = torch.arange(S).repeat(B, 1)
+    for act in (torch.float32, torch.bfloat16):
+        q = torch.randn(B, S, hq, D, generator=g).to(act)
+        k = torch.randn(B, S, hkv, D, generator=g).to(act)
+        v = torch.randn(B, S, hkv, D, generator=g).to(act)
+        q[0, ::3, 0, 1] = 1.0e5
+        v[0, ::5, 1, 2] = -7.0e4
+        shards = [tuple(layout.shard(t, r) for t in (q, k, v, pos)) for r in range(world)]
+        shards_d = [tuple(t.to(dev) for t in sh) for sh in shards]
+        rounded = [tuple(sp_ref.wire_round(t, torch.float16) for t in sh) for sh in shards]
+        for r in range(world):
+            got = cea.ulysses_scatter(*shards_d[r], _group(cea, shards_d, r, torch.float16),
+                                      layout.sizes, heads)
+            want = sp_ref.ulysses_scatter(rounded, heads, r)
+            torch.cuda.synchronize()
+            for a, b_ in zip(got, want):
+                assert torch.equal(a.cpu(), b_), (act, r)
+        if act == torch.float32:
+            assert rounded[0][0].abs().max().item() == 65504.0
+        else:
+            assert torch.equal(rounded[0][0], shards[0][0])
+
+
 def test_ulysses_workload_full_size(cea, dev):
     """The Ulysses workload's shape (65536 tokens, a 64/16-head model over sp=8, D=128,
     bf16): rank 0's scatter equals the head slices of the rank-order concatenation and the
