@@ -361,8 +361,11 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
   };
 
-  // ---- passes over the key block: list the tiles this workgroup needs, then stream them
-  for (int base = 0; base < p.ntiles; base += LIST_CAP) {
+  // ---- passes over the key block: list the tiles this workgroup needs, then stream them.
+  // Under the causal rule a workgroup whose rows all have position < 0 (padding) sees no key
+  // (a visible key needs 0 <= k_pos <= q_pos), so it goes straight to the epilogue.
+  const int npasses_end = p.causal && qmax_wg < 0 ? 0 : p.ntiles;
+  for (int base = 0; base < npasses_end; base += LIST_CAP) {
     const int span = min(LIST_CAP, p.ntiles - base);
     int n = 0;
     for (int r0 = 0; r0 < span; r0 += NTHREADS) {
