@@ -12,6 +12,7 @@ roofline of the dominant kernel measured live with HIP events on the launch stre
 CPU oracle timed on a bounded sample of the headline workload on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only ring]
+       python bench.py --trace-summary <rocprofv3 kernel_trace.csv> [--last N]
 """
 
 from __future__ import annotations
@@ -84,6 +85,11 @@ def _graph_timed(fn, steps: int, warmup: int, torch, per_graph: int = 20):
 
 
 def bench_ring(cea, torch, steps, warmup, dev):
+    """The headline: ``ring_attention`` over the four KV blocks of the ring share.  The K
+    timed steps are bracketed by host synchronisation (wall clock, ``value``) and by two HIP
+    events on the stream the kernels run on; the events give the GPU time of exactly those
+    steps, from which ``roofline`` takes the average duration of one ring step's attention
+    call (tile-summary pass + prefill kernel with its in-epilogue merge)."""
     w = cea.workloads.ring_share(device=dev)
     comm = cea.LocalGroup(w.layout.num_ranks, w.rank)
     for r, (k, v, p) in enumerate(w.blocks):
@@ -93,30 +99,21 @@ def bench_ring(cea, torch, steps, warmup, dev):
     def step():
         return cea.ring_attention(w.q, k0, v0, w.q_pos, p0, comm, w.kv_sizes)
 
-    sec = _timed(step, steps, warmup, torch)
-    # average duration of one attention call (tile summary + prefill kernel) over back-to-back
-    # ring passes, from two HIP events on the stream the kernels run on (an event pair around
-    # every launch would add its own gap and cache flush to each launch)
+    for _ in range(warmup):
+        step()
     stream = torch.cuda.current_stream(dev)
-    out = torch.zeros(w.q.shape, dtype=torch.float32, device=dev)
-    lse = torch.full((1, w.q.shape[2], w.q.shape[1]), float("-inf"), device=dev)
-
-    def ring_pass():
-        for i, src in enumerate(w.ring_order):
-            k, v, p = w.blocks[src]
-            cea.attention_with_lse_into(out, lse, w.q, k, v, w.q_pos, p, accumulate=i > 0)
-
-    passes = max(3, steps // 2)
-    ring_pass()
-    torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     a.record(stream)
-    for _ in range(passes):
-        ring_pass()
+    for _ in range(steps):
+        step()
     b.record(stream)
     torch.cuda.synchronize()
-    launch_ms = a.elapsed_time(b) / (passes * len(w.ring_order))
-    flop_launch = w.flop / len(w.ring_order)
+    sec = (time.perf_counter() - t0) / steps
+    n_launch = len(w.ring_order)
+    launch_ms = a.elapsed_time(b) / (steps * n_launch)
+    flop_launch = w.flop / n_launch
     achieved = flop_launch / (launch_ms * 1e-3) / 1e12
     tflops = w.flop / sec / 1e12
     return w, sec, tflops, {
@@ -128,6 +125,7 @@ def bench_ring(cea, torch, steps, warmup, dev):
         "traffic": _measured_traffic("attn_prefill_ring_share"),
         "kernel": "attn_prefill_kernel<bf16,128> (+ tile summary pass), one ring step",
         "launch_ms": round(launch_ms, 4),
+        "launches": steps * n_launch,
         "flop_per_launch": int(flop_launch),
     }
 
@@ -266,35 +264,154 @@ def bench_f32_split(cea, torch, steps, warmup, dev):
             "workload": "f32 attention B=1 8/8 heads S=512 D=64 causal, 2-way KV split + merge"}
 
 
-def cpu_baseline(cea, torch, budget_s: float = 20.0):
-    """The CPU oracle (restatement of the reference's CPU route) on a bounded sample of the
-    headline workload: growing sets of query rows from both zigzag halves, against all four
-    KV blocks in ring order, until about ``budget_s`` seconds of CPU work."""
+def _median_time(fn, reps: int) -> float:
+    fn()  # one warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def _host_info(threads: int) -> dict:
+    import platform
+
+    model = platform.processor() or ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    import torch
+
+    return {"threads": threads, "os_cpu_count": os.cpu_count(), "affinity_cpus": affinity,
+            "cpu_model": model, "torch": torch.__version__}
+
+
+def cpu_baseline(cea, torch):
+    """The CPU oracle (the restatement of the reference's CPU route: f32 upcast, additive
+    -inf bias per query chunk, torch's CPU flash-attention operator, the reference's merges
+    and layer-op sequence) on the five workloads, timed on this host's cores with
+    ``time.perf_counter``: one warm-up, then the median of N repetitions (N = 5 for the f32
+    split-merge, the layer ops and the decode sample; 1 for the ring share, which runs in
+    full; the Ulysses share on a stated subset of query rows).  Rates use the same
+    algorithmic FLOP / byte counts as the GPU lines.  The top-level fields are the headline
+    ring share's."""
+    from oracle import attention_ref as ref
+    from oracle import layers_ref as lref
     from oracle import sp_ref
 
-    w = cea.workloads.ring_share(device="cpu")
-    # the host share of one GPU: OMP_NUM_THREADS where set, else at most 16 cores
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    # the process's CPU share: OMP_NUM_THREADS where the host sets it (the GPU box gives each
+    # GPU 16 cores), else every core this process may run on
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or avail
     torch.set_num_threads(threads)
-    half = w.q.shape[1] // 2
-    rows, done_s, done_flop, sample = 64, 0.0, 0, []
-    while done_s < budget_s and rows <= half:
-        idx = torch.cat([torch.arange(0, rows), torch.arange(half, half + rows)])
-        q = w.q[:, idx]
-        qp = w.q_pos[:, idx]
-        t0 = time.perf_counter()
-        sp_ref.ring_share(q, qp, w.blocks, w.rank)
-        dt = time.perf_counter() - t0
-        pairs = sum(cea.workloads.visible_pairs(qp, w.blocks[r][2]) for r in w.ring_order)
-        done_s += dt
-        done_flop += 4 * w.q.shape[-1] * w.q.shape[2] * pairs
-        sample.append(2 * rows)
-        rows *= 2
-    return {"value": round(done_flop / done_s / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle ring share (CPU flash route, f32) for query-row subsets {sample} "
-                      f"of the 8192 local rows (half from each zigzag half) x 4 KV blocks; "
-                      f"{done_s:.1f} s, {done_flop:.3e} algorithmic FLOP"}
+    configs = {}
+
+    # f32 attention S=512, 8/8 heads, D=64, causal: KV halves + exact merge
+    w1 = cea.workloads.attn_f32_split(device="cpu")
+    h = w1.split
+
+    def c1():
+        a = ref.attention_with_lse(w1.q, w1.k[:, :h], w1.v[:, :h], w1.pos, w1.pos[:, :h], scale=w1.scale)
+        b = ref.attention_with_lse(w1.q, w1.k[:, h:], w1.v[:, h:], w1.pos, w1.pos[:, h:], scale=w1.scale)
+        return ref.merge_pair(a[0], a[1], b[0], b[1])
+
+    t = _median_time(c1, 5)
+    configs["attn_f32_split"] = {"value": round(w1.flop / t / 1e12, 4), "unit": "TFLOP/s",
+                                 "ms_per_step": round(t * 1e3, 3), "reps": 5,
+                                 "sample": "full workload (two KV halves + merge)"}
+
+    # bf16 RMSNorm+rotary [4096,4096] -> 32x128 and SiLU-gate [4096,14336]
+    w2 = cea.workloads.layer_ops(device="cpu")
+    inv = lref.inv_freq(w2.head_dim, w2.theta)
+    t = _median_time(lambda: lref.rmsnorm_rope(w2.x, w2.weight, w2.eps, w2.positions, inv, w2.heads), 5)
+    layer = {"rmsnorm_rope": {"value": round(w2.rmsnorm_rope_bytes / t / 1e9, 2), "unit": "GB/s",
+                              "ms_per_step": round(t * 1e3, 3)}}
+    t = _median_time(lambda: lref.silu_gate(w2.gate, w2.up), 5)
+    layer["silu_mul"] = {"value": round(w2.silu_bytes / t / 1e9, 2), "unit": "GB/s",
+                         "ms_per_step": round(t * 1e3, 3)}
+    layer["reps"] = 5
+    layer["sample"] = "full workload"
+    configs["layer_ops"] = layer
+    del w2
+
+    # ring share: all 8192 local rows against the four KV blocks, in full
+    w3 = cea.workloads.ring_share(device="cpu")
+    t0 = time.perf_counter()
+    sp_ref.ring_share(w3.q, w3.q_pos, w3.blocks, w3.rank)
+    t3 = time.perf_counter() - t0
+    ring = {"value": round(w3.flop / t3 / 1e12, 4), "unit": "TFLOP/s",
+            "ms_per_step": round(t3 * 1e3, 1), "reps": 1,
+            "sample": "full share: 8192 query rows x 4 KV blocks of 8192 in ring order"}
+    configs["ring_share"] = ring
+    del w3
+
+    # distributed-KV decode: 8 of the 32 sequences (every 4th), 4 partitions + merge
+    rows = list(range(0, 32, 4))
+    w4 = cea.workloads.kv_decode(device="cpu", batch=rows)
+    parts = w4.partitions()
+    t = _median_time(lambda: sp_ref.distributed_kv_share(w4.q, w4.q_pos, parts), 5)
+    nb = w4.bytes
+    configs["kv_decode"] = {"value": round(nb / t / 1e9, 2), "unit": "GB/s",
+                            "ms_per_step": round(t * 1e3, 2), "reps": 5, "bytes": nb,
+                            "sample": f"sequences {rows} of the 32 (their valid K/V, partials and "
+                                      "output bytes), 4 partitions + exact merge"}
+    del w4, parts
+
+    # Ulysses share: 32 chunks of 64 query rows, evenly spaced over the valid tokens, against
+    # all 65536 keys (the oracle's query chunk is 64 rows at this key count)
+    w5 = cea.workloads.ulysses_share(device="cpu")
+    L = w5.valid
+    starts = torch.linspace(0, max(0, L - 64), 32).round().to(torch.int64)
+    idx = torch.cat([torch.arange(int(s0), int(s0) + 64) for s0 in starts])
+    qs, ps = w5.q[:, idx], w5.pos[:, idx]
+    t = _median_time(lambda: ref.attention_with_lse(qs, w5.k, w5.v, ps, w5.pos, kv_map=w5.kv_map), 1)
+    pairs = cea.workloads.visible_pairs(ps, w5.pos)
+    flop = 4 * w5.q.shape[-1] * w5.q.shape[2] * pairs
+    configs["ulysses_share"] = {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s",
+                                "seconds": round(t, 3), "reps": 1,
+                                "sample": f"{idx.numel()} of {L} valid query rows (32 evenly "
+                                          "spaced chunks of 64) x 65536 keys"}
+    del w5
+
+    return {"value": ring["value"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": ring["sample"] + "; the other workloads under 'configs'",
+            "host": _host_info(threads), "configs": configs}
+
+
+def summarize_kernel_trace(path: str, last: int) -> str:
+    """Per-kernel duration statistics of the last ``last`` dispatches of each kernel in a
+    rocprofv3 kernel-trace CSV (``--kernel-trace --output-format csv``): the dispatches of a
+    bench run's timed steps, without its warm-up."""
+    import csv
+
+    rows = {}
+    with open(path, newline="") as f:
+        for rec in csv.DictReader(f):
+            name = rec.get("Kernel_Name") or rec.get("KernelName") or "?"
+            t0 = int(rec.get("Start_Timestamp") or rec.get("BeginNs"))
+            t1 = int(rec.get("End_Timestamp") or rec.get("EndNs"))
+            rows.setdefault(name, []).append((t0, t1 - t0))
+    lines = ["| kernel | dispatches (all) | averaged | avg us | min us | max us |",
+             "|---|---|---|---|---|---|"]
+    for name, recs in sorted(rows.items(), key=lambda kv: -sum(d for _, d in kv[1])):
+        recs.sort()
+        tail = [d for _, d in recs[-last:]]
+        short = name if len(name) < 90 else name[:87] + "..."
+        lines.append(f"| `{short}` | {len(recs)} | {len(tail)} | {sum(tail) / len(tail) / 1e3:.2f} "
+                     f"| {min(tail) / 1e3:.2f} | {max(tail) / 1e3:.2f} |")
+    return "\n".join(lines)
 
 
 def main() -> int:
@@ -304,10 +421,16 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,kvappend,ulysses,wire,f32")
-    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--trace-summary", default="", metavar="CSV",
+                    help="only summarise a rocprofv3 kernel-trace CSV (the last --last "
+                         "dispatches of every kernel) and exit")
+    ap.add_argument("--last", type=int, default=80)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(summarize_kernel_trace(args.trace_summary, args.last))
+        return 0
     if args.calib_copy:
         import torch
 
@@ -354,7 +477,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline (oracle)")
-        cpu = cpu_baseline(cea, torch, args.cpu_budget)
+        cpu = cpu_baseline(cea, torch)
 
     result = {
         "metric": "attn prefill TFLOP/s (% MFMA peak); decode+merge GB/s (% HBM peak)",

@@ -175,13 +175,14 @@ def attention_with_lse(
     Sk = k.shape[1]
     if Sk == 0 or q.shape[1] == 0:
         return _empty_result(q, acc)
+    if kv_block is not None and kv_block < 1:
+        # the reference's range(0, Sk, 0) raises; a negative block size is rejected too
+        raise ValueError("kv_block must be positive")
     q, k, v, q_pos, k_pos, mapping = _prepare(q, k, v, q_pos, k_pos, kv_map)
     B, Sq, Hq, D = q.shape
     out = torch.empty(B, Sq, Hq, D, dtype=acc, device=q.device)
     lse = torch.empty(B, Hq, Sq, dtype=acc, device=q.device)
     if kv_block is not None and kv_block < Sk:
-        if kv_block < 1:
-            raise ValueError("kv_block must be positive")
         out.zero_()
         lse.fill_(float("-inf"))
         for start in range(0, Sk, kv_block):

@@ -231,9 +231,13 @@ static bool use_decode(const AttnParams& p) {
   return ((uintptr_t)p.q & 15) == 0 && ((uintptr_t)p.k & 15) == 0 && ((uintptr_t)p.v & 15) == 0;
 }
 
-// Runs one attention call with a prepared parameter block.
-static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t st) {
-  if (p.Sk > 0 && use_decode(p)) return run_decode(&p, 1, nullptr, nullptr, ws, ws_bytes, st);
+// Runs one attention call with a prepared parameter block.  allow_decode = false keeps the
+// call off the split-KV decode kernels, whose workspace (chunk partials) is larger than the
+// tile summaries the other kernels need.
+static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t st,
+                         bool allow_decode = true) {
+  if (allow_decode && p.Sk > 0 && use_decode(p))
+    return run_decode(&p, 1, nullptr, nullptr, ws, ws_bytes, st);
   if (p.Sk > 0 && prefill_mfma_supported(p)) {
     const size_t need = tile_bytes(p.B, p.Sk);
     CEA_REQUIRE(ws != nullptr && ws_bytes >= need, CEA_ENOSPACE,
@@ -692,7 +696,9 @@ int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* 
     rc = make_attn_params(&p, q, &ks[i], &vs[i], q_pos, &k_pos_s[i], causal, scale, kv_map,
                           kv_map_len, &po[i], &pl[i], 0);
     if (rc) return rc;
-    rc = run_attention(p, tiles, tile_bytes(B, maxsk), st);
+    // the workspace past the tile summaries holds the partials: this partition must not
+    // take the decode route (its chunk partials would not fit in the tile slice)
+    rc = run_attention(p, tiles, tile_bytes(B, maxsk), st, false);
     if (rc) return rc;
   }
   if (n == 1 && out->data == po[0].data) return CEA_OK;

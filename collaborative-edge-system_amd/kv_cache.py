@@ -6,7 +6,8 @@ The reference stores keys/values head-major ``[B, H, capacity, D]`` and appends 
 (``apply_rotary``, llama.py:161, 196, 205, 208).  :meth:`LayerKVCache.append_rotary` does
 rotation, both copies and the position update in one kernel (``cea_kv_append``), with the
 rounding points of ``apply_rotary``; :meth:`LayerKVCache.append` is the plain append.
-Growth keeps the reference's policy and copies (cache.py:39-49).
+Keys and values share one allocation; capacity grows by the reference's rule
+(cache.py:39-49).
 """
 
 from __future__ import annotations
@@ -53,71 +54,94 @@ def kv_append(cache_k: torch.Tensor, cache_v: torch.Tensor, cache_pos: torch.Ten
 class LayerKVCache:
     """Growable key/value cache of one attention layer on one rank (cache.py:11-85).
 
-    Keys/values are stored head-major ``[B, H_local, capacity, D]``; :meth:`view` returns
-    token-major ``[B, T, H_local, D]`` views of the same memory.  Positions of the cached
-    tokens are kept as ``[B, capacity]`` (``-1`` in unused slots).
+    Keys and values live in one device allocation ``[2, B, H, capacity, D]`` (``k`` and ``v``
+    are its two head-major halves ``[B, H, capacity, D]``), positions in ``[B, capacity]``
+    with ``-1`` in unused slots.  Appends write through the fused kernel (``cea_kv_append``);
+    :meth:`view` hands out token-major ``[B, T, H, D]`` views of the filled prefix, which the
+    attention kernels read in place.
+
+    Capacity follows the reference's policy, since it decides when memory is reallocated:
+    when an append does not fit, the cache grows to ``max(needed + reserve,
+    int(1.5 * capacity))`` slots (cache.py:39-49) and the filled prefix moves over.  K and V
+    must share their shape (every model of the reference has them so).
     """
 
     def __init__(self, reserve: int = 0) -> None:
-        self.k: Optional[torch.Tensor] = None  # [B, H, capacity, D]
-        self.v: Optional[torch.Tensor] = None
-        self.pos: Optional[torch.Tensor] = None  # [B, capacity]
-        self.length = 0
         self.reserve = max(0, int(reserve))
+        self.length = 0
+        self._kv: Optional[torch.Tensor] = None    # [2, B, H, capacity, D]
+        self._pos: Optional[torch.Tensor] = None   # [B, capacity], -1 = unused
+
+    # -- storage -------------------------------------------------------------------------
+    @property
+    def k(self) -> Optional[torch.Tensor]:
+        return None if self._kv is None else self._kv[0]
+
+    @property
+    def v(self) -> Optional[torch.Tensor]:
+        return None if self._kv is None else self._kv[1]
+
+    @property
+    def pos(self) -> Optional[torch.Tensor]:
+        return self._pos
+
+    @property
+    def capacity(self) -> int:
+        return 0 if self._kv is None else int(self._kv.shape[3])
 
     def __len__(self) -> int:
         return self.length
 
-    @property
-    def capacity(self) -> int:
-        return 0 if self.k is None else self.k.shape[2]
-
-    def _grow(self, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor, needed: int) -> None:
-        # cache.py:39-49: max(needed + reserve, 1.5 x capacity) slots, old content copied,
-        # unused position slots -1
-        capacity = max(needed + self.reserve, int(self.capacity * 1.5))
+    def _reserve_for(self, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor, extra: int) -> None:
+        """Makes room for ``extra`` more tokens shaped like ``k`` / ``v``."""
+        if tuple(v.shape) != tuple(k.shape):
+            raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must have one shape")
+        want = self.length + extra
+        if self._kv is not None and want <= self.capacity:
+            return
+        slots = max(want + self.reserve, int(self.capacity * 1.5))
         B, _, H, D = k.shape
-        new_k = k.new_empty((B, H, capacity, D))
-        new_v = v.new_empty((B, v.shape[2], capacity, v.shape[3]))
-        new_pos = pos.new_full((B, capacity), -1, dtype=torch.int64)
+        kv = k.new_empty((2, B, H, slots, D))
+        pos_new = torch.full((B, slots), -1, dtype=torch.int64, device=k.device)
         if self.length:
-            new_k[:, :, : self.length] = self.k[:, :, : self.length]
-            new_v[:, :, : self.length] = self.v[:, :, : self.length]
-            new_pos[:, : self.length] = self.pos[:, : self.length]
-        self.k, self.v, self.pos = new_k, new_v, new_pos
+            kv[:, :, :, : self.length].copy_(self._kv[:, :, :, : self.length])
+            pos_new[:, : self.length].copy_(self._pos[:, : self.length])
+        self._kv, self._pos = kv, pos_new
 
-    def _append(self, k, v, pos, cos, sin) -> None:
+    def _write(self, k, v, pos, cos, sin) -> None:
         n = k.shape[1]
         if n == 0:
             return
-        if self.k is None or self.length + n > self.capacity:
-            self._grow(k, v, pos, self.length + n)
-        kv_append(self.k, self.v, self.pos, self.length, k, v, pos, cos, sin)
+        self._reserve_for(k, v, pos, n)
+        kv_append(self._kv[0], self._kv[1], self._pos, self.length, k, v, pos, cos, sin)
         self.length += n
 
+    # -- the reference's interface ---------------------------------------------------------
     def append(self, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor) -> None:
         """Append token-major ``k``/``v`` (``[B, n, H, D]``) and their positions (cache.py:51-62)."""
-        self._append(k, v, pos, None, None)
+        self._write(k, v, pos, None, None)
 
     def append_rotary(self, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor,
                       cos: torch.Tensor, sin: torch.Tensor) -> None:
         """``append(apply_rotary(k, cos, sin), v, pos)`` in one kernel (``cos``/``sin``
         ``[B, n, D]`` as RotaryEmbedding returns them)."""
-        self._append(k, v, pos, cos, sin)
+        self._write(k, v, pos, cos, sin)
 
     def view(self, like_k: Optional[torch.Tensor] = None, like_pos: Optional[torch.Tensor] = None
              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """Cached ``(k, v, pos)`` as token-major views (cache.py:64-75)."""
-        if self.k is None:
+        """The cached ``(k, v, pos)`` as token-major views of the filled prefix (cache.py:64-75);
+        before the first append, empty tensors shaped after ``like_k`` / ``like_pos``."""
+        if self._kv is None:
             if like_k is None or like_pos is None:
-                raise RuntimeError("empty cache: provide templates to build empty views")
-            empty = like_k.new_empty((like_k.shape[0], 0) + tuple(like_k.shape[2:]))
-            return empty, empty, like_pos.new_empty((like_pos.shape[0], 0))
-        n = self.length
-        return self.k[:, :, :n].transpose(1, 2), self.v[:, :, :n].transpose(1, 2), self.pos[:, :n]
+                raise RuntimeError("nothing cached yet: pass like_k and like_pos to shape empty views")
+            none_k = like_k.new_empty((like_k.shape[0], 0, *like_k.shape[2:]))
+            return none_k, none_k, like_pos.new_empty((like_pos.shape[0], 0))
+        filled = self._kv[:, :, :, : self.length].transpose(2, 3)   # [2, B, T, H, D]
+        return filled[0], filled[1], self._pos[:, : self.length]
 
     def nbytes(self) -> int:
-        if self.k is None:
+        """Bytes of the cached tokens' keys and values (not the unused slots)."""
+        if self._kv is None:
             return 0
-        per_token = (self.k[:, :, :1].numel() + self.v[:, :, :1].numel()) * self.k.element_size()
-        return per_token * self.length
+        _, B, H, _, D = self._kv.shape
+        return 2 * B * H * D * self.length * self._kv.element_size()

@@ -107,10 +107,18 @@ class LocalGroup:
 
 
 def _kv_from(comm: LocalGroup, src: int, own: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]):
+    """The KV block of rank ``src`` as the ring delivers it: received blocks went through
+    the wire dtype (sequence_parallel.py:103, 127), the own block did not."""
     if src == comm.rank:
         return own
     s = comm.shard(src)
     return comm.received(s["k"]), comm.received(s["v"]), s["pos"]
+
+
+def _raw_kv(comm: LocalGroup, src: int):
+    """The KV partition rank ``src`` stores, untouched by any wire rounding."""
+    s = comm.shard(src)
+    return s["k"], s["v"], s["pos"]
 
 
 # --------------------------------------------------------------------------------------
@@ -159,6 +167,8 @@ def ring_attention_with_lse(
     (``_final``: a tensor that receives the merged output of the last merge instead; ``out``
     is then unspecified)."""
     n, r = comm.size, comm.rank
+    if kv_block is not None and kv_block < 1:
+        raise ValueError("kv_block must be positive")
     if n == 1:
         return attention_with_lse(q, k, v, q_pos, k_pos, causal=causal, scale=scale,
                                   kv_map=kv_map, kv_block=kv_block)
@@ -176,7 +186,7 @@ def ring_attention_with_lse(
         if kb.shape[1] != kv_sizes[(r - step) % n]:
             raise ValueError(f"kv_sizes {list(kv_sizes)} inconsistent with the block of rank {(r - step) % n}")
         blk = kv_block if kv_block is not None and kv_block < kb.shape[1] else kb.shape[1]
-        for start in range(0, kb.shape[1], max(1, blk)):
+        for start in range(0, kb.shape[1], blk):
             end = min(start + blk, kb.shape[1])
             launches.append((kb[:, start:end], vb[:, start:end], pb[:, start:end]))
     if not launches:  # no rank held a key: the merge's neutral element
@@ -296,8 +306,10 @@ def distributed_kv_attention(
         o, _ = attention_with_lse(q, k_local, v_local, q_pos, k_pos_local, causal=causal,
                                   scale=scale, kv_map=kv_map, kv_block=kv_block)
         return o.to(q.dtype)
+    # every rank attends to the partition it stores at full precision; only the f32
+    # (out | lse) message crosses the wire, uncompressed (sequence_parallel.py:270-279)
     own = (k_local, v_local, k_pos_local)
-    parts = [_kv_from(comm, i, own) for i in range(comm.size)]  # rank order, as all_gather
+    parts = [own if i == comm.rank else _raw_kv(comm, i) for i in range(comm.size)]
     if wire:
         B, Sq, Hq, D = q.shape
         gathered = torch.empty(comm.size, B, Sq, Hq, D + 1, dtype=accumulation_dtype(q.dtype),

@@ -182,3 +182,61 @@ def test_kv_decode_workload_subset_matches_oracle(cea, dev):
     assert out.dtype == torch.bfloat16
     err = (out.cpu().float() - ro.float()).abs().max().item()
     assert err <= 2e-2, err
+
+
+@pytest.mark.parametrize("wire_kv", [False, True], ids=["fused", "packed"])
+def test_distributed_kv_ignores_activation_wire_dtype(cea, dev, wire_kv):
+    """Distributed-KV decoding moves no K/V: each rank attends to the partition it stores at
+    full precision and only the f32 (out | lse) message is all-gathered, uncompressed
+    (sequence_parallel.py:270-279).  With a float16 activation wire and f64 activations whose
+    keys / values exceed the float16 range (a rounded or saturated K/V would move the result
+    by far more than the f64 tolerance), the result must still be the oracle's."""
+    world, B, T, hq, hkv, d = 3, 2, 300, 4, 2, 64
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(B, 1, hq, d, generator=g, dtype=torch.float64) * 0.01
+    k = torch.randn(B, T, hkv, d, generator=g, dtype=torch.float64)
+    v = torch.randn(B, T, hkv, d, generator=g, dtype=torch.float64)
+    k[:, ::11, :, 2] = 8.0e4
+    v[:, ::7, :, 1] = -1.0e5
+    pos = torch.arange(T).repeat(B, 1)
+    qpos = torch.full((B, 1), T - 1)
+    sizes = cea.split_sizes(T, [0.5, 0.3, 0.2])
+    group = cea.LocalGroup(world, 1, wire_dtype=torch.float16)
+    parts, start = [], 0
+    for r, n in enumerate(sizes):
+        parts.append((k[:, start:start + n], v[:, start:start + n], pos[:, start:start + n]))
+        group.set_shard(r, k=parts[-1][0].to(dev), v=parts[-1][1].to(dev), pos=parts[-1][2].to(dev))
+        start += n
+    own = [t.to(dev) for t in parts[1]]
+    out = cea.distributed_kv_attention(q.to(dev), own[0], own[1], qpos.to(dev), own[2], group,
+                                       wire=wire_kv)
+    ro = sp_ref.distributed_kv_share(q, qpos, parts)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float64
+    err = (out.cpu() - ro).abs().max().item()
+    assert err <= 1e-10, err
+    # the same K/V rounded through float16 on the way would not pass
+    rounded = [(sp_ref.wire_round(kk, torch.float16), sp_ref.wire_round(vv, torch.float16), pp)
+               for kk, vv, pp in parts]
+    assert (sp_ref.distributed_kv_share(q, qpos, rounded) - ro).abs().max().item() > 1.0
+
+
+def test_partitioned_fallback_with_many_chunks(cea, dev):
+    """Four partitions whose key chunks together exceed what one split-KV launch takes
+    (each partition alone would fit): every partition runs as its own attention call inside
+    the workspace the library asked for, then the exact merge."""
+    B, hq, hkv, d, n = 1, 4, 1, 128, 300_000
+    g = torch.Generator().manual_seed(13)
+    q = torch.randn(B, 1, hq, d, generator=g).to(torch.bfloat16)
+    parts_cpu = []
+    for i in range(4):
+        k = torch.randn(B, n, hkv, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(B, n, hkv, d, generator=g).to(torch.bfloat16)
+        p = torch.arange(i * n, (i + 1) * n).view(1, n)
+        parts_cpu.append((k, v, p))
+    qpos = torch.tensor([[4 * n]])
+    parts = [tuple(t.to(dev) for t in pc) for pc in parts_cpu]
+    out, lse = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts, return_lse=True)
+    ro, rl, _ = sp_ref.distributed_kv_share(q, qpos, parts_cpu, with_parts=True)
+    torch.cuda.synchronize()
+    assert_attention_close(out, lse, ro.float(), rl, torch.bfloat16, "4 x 300k keys")

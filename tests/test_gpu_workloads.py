@@ -2,16 +2,15 @@
 
 * f32 attention (S=512, 8 heads, D=64) and its 2-way key split merged: both against the
   oracle, normwise rel <= 1e-5;
-* zigzag ring share (sp=4, 32768 tokens, GQA 32/8, D=128, bf16): the full share on the GPU,
-  checked against the oracle's ring loop on a spread of query rows of both zigzag halves
-  (rows are independent), and against one attention call over all 32768 keys (a merge of
-  disjoint key sets is exact; the two paths round the probabilities to bf16 relative to
-  different running maxima, so out agrees within 1e-3 and lse, formed in f32, within 1e-4);
-* distributed-KV decode (B=32, cache 32768, 4 partitions): all 32 sequences against one
-  attention call over the whole cache (same property), and 4 sequences against the oracle
-  (in tests/test_gpu_sequence_parallel.py);
+* zigzag ring share (sp=4, 32768 tokens, GQA 32/8, D=128, bf16): all 8192 query rows
+  against the oracle's ring loop, and against one attention call over all 32768 keys (a
+  merge of disjoint key sets is exact; the two paths round the probabilities to bf16
+  relative to different running maxima, so out agrees within 1e-3 and lse, formed in f32,
+  within 1e-4);
+* distributed-KV decode (B=32, cache 32768, 4 partitions): all 32 sequences against the
+  oracle, and against one attention call over the whole cache (same property);
 * Ulysses share (65536 tokens, 8/2 heads, right padding): the full local attention against
-  the oracle on a spread of query rows, plus out and lse;
+  the oracle on 1024 query rows spread over the valid tokens and 64 padded rows;
 * linearity in V of the attention output at a production shape.
 bf16 tolerances are the ones of tests/_cases.py.
 """
@@ -50,6 +49,8 @@ def _spread(n, rows, *, seed=0):
 
 
 def test_ring_share_full_size(cea, dev):
+    """All 8192 query rows of the ring share against the oracle's ring loop (skip rule,
+    ring order, pairwise merges), plus the merge property against one call over all keys."""
     w = cea.workloads.ring_share(device="cpu")
     blocks = [(k.to(dev), v.to(dev), p.to(dev)) for k, v, p in w.blocks]
     group = cea.LocalGroup(4, 0)
@@ -58,6 +59,7 @@ def test_ring_share_full_size(cea, dev):
     qd, qpd = w.q.to(dev), w.q_pos.to(dev)
     out, lse = cea.sequence_parallel.ring_attention_with_lse(qd, blocks[0][0], blocks[0][1], qpd,
                                                              blocks[0][2], group, w.kv_sizes)
+    final = cea.ring_attention(qd, blocks[0][0], blocks[0][1], qpd, blocks[0][2], group, w.kv_sizes)
     # one call over all keys (disjoint key sets merged == unsplit)
     kall = torch.cat([b[0] for b in blocks], 1)
     vall = torch.cat([b[1] for b in blocks], 1)
@@ -68,33 +70,56 @@ def test_ring_share_full_size(cea, dev):
     assert torch.equal(torch.isfinite(lse), fin)
     assert (out - one).abs().max().item() <= 1e-3
     assert (lse[fin] - one_lse[fin]).abs().max().item() <= 1e-4
-    # oracle on 24 rows of each zigzag half
-    rows = torch.cat([_spread(4096, 24, seed=1), 4096 + _spread(4096, 24, seed=2)])
-    ro, rl = sp_ref.ring_share(w.q[:, rows], w.q_pos[:, rows], w.blocks, 0, with_lse=True)
-    assert_attention_close(out[:, rows.to(dev)], lse[:, :, rows.to(dev)], ro, rl, torch.bfloat16, "ring rows")
+    ro, rl = sp_ref.ring_share(w.q, w.q_pos, w.blocks, 0, with_lse=True)
+    assert_attention_close(out, lse, ro, rl, torch.bfloat16, "ring share, all rows")
+    # the bf16 result of ring_attention (last merge cast in the kernel) is the f32 result cast
+    assert final.dtype == torch.bfloat16
+    assert torch.equal(final.cpu(), out.to(torch.bfloat16).cpu())
+    assert (final.float().cpu() - ro).abs().max().item() <= 2e-2
 
 
-def test_kv_decode_full_batch_equals_single_call(cea, dev):
-    w = cea.workloads.kv_decode(device=dev)
-    parts = w.partitions()
-    out, lse = cea.partitioned_attention(w.q, w.q_pos, parts, return_lse=True)
-    k = w.cache_k.transpose(1, 2)
-    v = w.cache_v.transpose(1, 2)
-    one, one_lse = cea.attention_with_lse(w.q, k, v, w.q_pos, w.k_pos)
+def test_kv_decode_full_batch_against_oracle(cea, dev):
+    """All 32 sequences of the distributed-KV decode workload against the oracle (each
+    partition's attention and the merge, sequence by sequence), plus the merge property
+    against one call over the whole cache."""
+    w = cea.workloads.kv_decode(device="cpu")
+    qd, qpd = w.q.to(dev), w.q_pos.to(dev)
+    ck, cv, kp = w.cache_k.to(dev), w.cache_v.to(dev), w.k_pos.to(dev)
+    parts, start = [], 0
+    for n in w.part_sizes:
+        parts.append((ck[:, :, start:start + n].transpose(1, 2),
+                      cv[:, :, start:start + n].transpose(1, 2), kp[:, start:start + n]))
+        start += n
+    out, lse = cea.partitioned_attention(qd, qpd, parts, return_lse=True)
+    bf = cea.partitioned_attention(qd, qpd, parts)
+    one, one_lse = cea.attention_with_lse(qd, ck.transpose(1, 2), cv.transpose(1, 2), qpd, kp)
     torch.cuda.synchronize()
     assert torch.isfinite(lse).all()
     assert (out - one).abs().max().item() <= 1e-3
     assert (lse - one_lse).abs().max().item() <= 1e-4
+    out_c, lse_c, bf_c = out.cpu(), lse.cpu(), bf.cpu()
+    cpu_parts = w.partitions()
+    for b in range(w.q.shape[0]):
+        sl = slice(b, b + 1)
+        pb = [(k[sl], v[sl], p[sl]) for k, v, p in cpu_parts]
+        rb, rl, partial = sp_ref.distributed_kv_share(w.q[sl], w.q_pos[sl], pb, with_parts=True)
+        ro, _ = ref.merge_many([x[0] for x in partial], [x[1] for x in partial])
+        assert_attention_close(out_c[sl], lse_c[sl], ro, rl, torch.bfloat16, f"decode seq {b}")
+        assert (bf_c[sl].float() - rb.float()).abs().max().item() <= 2e-2, f"decode seq {b} bf16"
 
 
 def test_ulysses_share_full_size(cea, dev):
+    """The Ulysses local attention (65536 tokens, right padding) against the oracle on 1088
+    query rows: 1024 spread evenly over the valid tokens of the packed sequences, 64 in the
+    padding; padded rows are exactly (0, -inf)."""
     w = cea.workloads.ulysses_share(device="cpu")
     qd, kd, vd, pd = (t.to(dev) for t in (w.q, w.k, w.v, w.pos))
     out, lse = cea.attention_with_lse(qd, kd, vd, pd, pd, kv_map=w.kv_map)
     plain = cea.attention_fn(qd, kd, vd, pd, pd, kv_map=w.kv_map)
     torch.cuda.synchronize()
     L = sum(w.lengths)
-    rows = torch.cat([_spread(L, 40, seed=3), L + _spread(65536 - L, 8, seed=4)])
+    valid_rows = torch.linspace(0, L - 1, 1024).round().to(torch.int64).unique()
+    rows = torch.cat([valid_rows, L + _spread(65536 - L, 64, seed=4)])
     ro, rl = ref.attention_with_lse(w.q[:, rows], w.k, w.v, w.pos[:, rows], w.pos, kv_map=w.kv_map)
     rd = rows.to(dev)
     assert_attention_close(out[:, rd], lse[:, :, rd], ro, rl, torch.bfloat16, "ulysses rows")

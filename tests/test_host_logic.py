@@ -337,3 +337,17 @@ def test_wire_pin_rejects_planted_mistakes():
 
     assert not _wire_pin(no_clamp)
     assert not _wire_pin(always)
+
+
+def test_ring_attention_rejects_nonpositive_kv_block(cea):
+    """A block size below one is an error (the reference's range() with step 0 raises), not a
+    silent empty loop that leaves the running (out, lse) uninitialised."""
+    q = torch.zeros(1, 4, 2, 8)
+    kv = torch.zeros(1, 4, 2, 8)
+    pos = torch.arange(4).view(1, 4)
+    group = cea.LocalGroup(2, 0)
+    for bad in (0, -3):
+        with pytest.raises(ValueError):
+            cea.ring_attention(q, kv, kv, pos, pos, group, [4, 4], kv_block=bad)
+        with pytest.raises(ValueError):
+            cea.attention_with_lse(q, kv, kv, pos, pos, kv_block=bad)
