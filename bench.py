@@ -207,8 +207,10 @@ def bench_wire(cea, torch, steps, warmup, dev):
                               "us_per_step": round(sec * 1e6, 2), "bytes": nb}
     outs = [torch.randn(1, S, h.q_count, D, generator=g, device=dev, dtype=torch.bfloat16)
             for h in heads]
-    sec = _graph_timed(lambda: cea.ulysses_gather(outs, grp, layout.sizes, heads), steps, warmup,
-                       torch, per_graph=10)
+    for j, o in enumerate(outs):  # what the other ranks send back
+        grp.set_shard(j, out_heads=o)
+    sec = _graph_timed(lambda: cea.ulysses_gather(outs[0], grp, layout.sizes, heads), steps,
+                       warmup, torch, per_graph=10)
     nb = 2 * (S // world) * 64 * D * 2
     res["ulysses_gather"] = {"value": round(nb / sec / 1e9, 1), "unit": "GB/s",
                              "frac": round(nb / sec / 1e9 / PEAK_HBM_GBS, 4),
@@ -219,8 +221,8 @@ def bench_wire(cea, torch, steps, warmup, dev):
     comm = cea.LocalGroup(len(parts), 0)
     for r, (kk, vv, pp) in enumerate(parts):
         comm.set_shard(r, k=kk, v=vv, pos=pp)
-    sec = _timed(lambda: cea.distributed_kv_attention(w.q, *parts[0][:2], w.q_pos, parts[0][2],
-                                                      comm, wire=True), steps, warmup, torch)
+    sec = _timed(lambda: cea.distributed_kv_attention_packed(w.q, *parts[0][:2], w.q_pos,
+                                                             parts[0][2], comm), steps, warmup, torch)
     B, Sq, Hq, _ = w.q.shape
     gathered = torch.randn(len(parts), B, Sq, Hq, D + 1, device=dev)
     msec = _graph_timed(lambda: cea.merge_packed(gathered, out_dtype=torch.bfloat16), steps,

@@ -13,9 +13,13 @@ Import with ``importlib.import_module("collaborative-edge-system_amd")``.  Modul
 * :mod:`.projection` - the fused Q/K/V and gate/up projections (torch's GEMM, column views)
   (collab_infer/parallel/tensor_parallel.py:264-320)
 * :mod:`.workloads` - seeded inputs of the five measured workloads
+* :mod:`.parallel` / :mod:`.models` - the reference's import paths
+  (``parallel.attention``, ``parallel.sequence_parallel``, ``parallel.partition``,
+  ``models.llama``, ``models.cache``) with its public names and signatures
 """
 
 from . import _native, attention, kv_cache, layers, partition, projection, sequence_parallel, workloads  # noqa: F401
+from . import models, parallel  # noqa: F401
 from .attention import (  # noqa: F401
     MASK_CHUNK_ELEMENTS,
     accumulation_dtype,
@@ -32,12 +36,24 @@ from .attention import (  # noqa: F401
     visibility_mask,
 )
 from .kv_cache import LayerKVCache, kv_append  # noqa: F401
-from .layers import RMSNorm, RotaryEmbedding, apply_rotary, rmsnorm, rmsnorm_rope, silu_mul  # noqa: F401
+from .layers import (  # noqa: F401
+    RMSNorm,
+    RotaryEmbedding,
+    apply_rotary,
+    gated_activation,
+    gated_mul,
+    rmsnorm,
+    rmsnorm_rope,
+    silu_mul,
+)
 from .partition import HeadShard, SequenceLayout, partition_heads, split_sizes  # noqa: F401
 from .projection import FusedColumnParallelLinear, fused_linear, linear  # noqa: F401
 from .sequence_parallel import (  # noqa: F401
     LocalGroup,
     distributed_kv_attention,
+    distributed_kv_attention_packed,
+    gather_heads,
+    gather_sequence,
     partitioned_attention,
     ring_attention,
     ulysses_attention,

@@ -832,15 +832,22 @@ int cea_rmsnorm_rope(const cea_tensor* x, const cea_tensor* weight, double eps,
                              (hipStream_t)stream);
 }
 
-int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, void* stream) {
+int cea_gated_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, int32_t act,
+                  void* stream) {
   int rc;
   if ((rc = check_tensor(gate, "gate", 2, -1, true))) return rc;
   if ((rc = check_tensor(up, "up", 2, gate->dtype, true))) return rc;
   if ((rc = check_tensor(out, "out", 2, gate->dtype, true))) return rc;
   for (int i = 0; i < 2; ++i)
     CEA_REQUIRE(up->size[i] == gate->size[i] && out->size[i] == gate->size[i], CEA_EINVAL,
-                "silu_mul: gate, up and out must have the same shape");
-  return launch_silu_mul(gate, up, out, (hipStream_t)stream);
+                "gated_mul: gate, up and out must have the same shape");
+  CEA_REQUIRE(act >= CEA_ACT_SILU && act <= CEA_ACT_RELU, CEA_EUNSUPPORTED,
+              "gated_mul: unknown activation %d", (int)act);
+  return launch_gated_mul(gate, up, out, act, (hipStream_t)stream);
+}
+
+int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, void* stream) {
+  return cea_gated_mul(gate, up, out, CEA_ACT_SILU, stream);
 }
 
 }  // extern "C"

@@ -152,7 +152,8 @@ int launch_kv_append(const cea_tensor* k, const cea_tensor* v, const cea_tensor*
 int launch_rmsnorm_rope(const cea_tensor* x, const cea_tensor* w, double eps,
                         const cea_tensor* pos, const cea_tensor* inv, int H, cea_tensor* o,
                         hipStream_t s);
-int launch_silu_mul(const cea_tensor* g, const cea_tensor* u, cea_tensor* o, hipStream_t s);
+int launch_gated_mul(const cea_tensor* g, const cea_tensor* u, cea_tensor* o, int act,
+                     hipStream_t s);
 int launch_attn_generic(const AttnParams& p, hipStream_t s);
 int launch_tile_info(const int64_t* k_pos, int64_t kps_b, int64_t kps_s, int32_t B, int32_t Sk,
                      TileInfo* tiles, int32_t ntiles, hipStream_t s);

@@ -3,7 +3,8 @@
 //   RMSNorm        collab_infer/models/llama.py:52-61
 //   rotary tables  collab_infer/models/llama.py:64-77 (inv_freq: models/config.py:165-189)
 //   apply_rotary   collab_infer/models/llama.py:80-88 (half-split, NeoX/HF convention)
-//   SiLU-gate      collab_infer/models/llama.py:45, 305, 316
+//   gated act      collab_infer/models/llama.py:44-49, 305, 316 (silu, gelu, gelu_pytorch_tanh,
+//                  relu)
 //
 // Rounding: the reference runs separate tensor ops, each rounding to the tensor dtype.  The
 // kernels keep every such rounding point (x*r -> T, w*that -> out dtype; x*cos -> T,
@@ -544,13 +545,43 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
-// SiLU-gate: out = silu(gate) * up with silu(g) = g / (1 + exp(-g)) rounded to T first.
-// ---------------------------------------------------------------------------------------
-template <typename T, int VEC>
-__global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ g, int64_t gs,
-                                                       const T* __restrict__ u, int64_t us,
-                                                       T* __restrict__ out, int64_t os,
-                                                       int64_t N, int I) {
+// Gated activations: out = act(gate) * up, act(gate) rounded to T first (the reference's
+// self.act(gate) * up, llama.py:44-49, 305: two separately rounded tensor ops; the
+// activation itself runs in f32 for bf16 / f16 / f32 and in f64 for f64, as torch's
+// elementwise kernels compute it):
+//   silu              g / (1 + exp(-g))
+//   gelu              (g * 0.5) * (1 + erf(g * (1/sqrt 2)))
+//   gelu_pytorch_tanh (0.5 * g) * (1 + tanh(sqrt(2/pi) * (g + 0.044715 * g^3)))
+//   relu              g when g > 0 or g is NaN, else 0
+template <typename M> __device__ __forceinline__ M erf_acc(M x);
+template <> __device__ __forceinline__ float erf_acc<float>(float x) { return erff(x); }
+template <> __device__ __forceinline__ double erf_acc<double>(double x) { return erf(x); }
+template <typename M> __device__ __forceinline__ M tanh_acc(M x);
+template <> __device__ __forceinline__ float tanh_acc<float>(float x) { return tanhf(x); }
+template <> __device__ __forceinline__ double tanh_acc<double>(double x) { return tanh(x); }
+
+template <int ACT, typename M> __device__ __forceinline__ M gate_act(M a) {
+  if constexpr (ACT == CEA_ACT_SILU) {
+    return div_rn(a, add_rn((M)1, exp_acc(-a)));
+  } else if constexpr (ACT == CEA_ACT_GELU) {
+    const M alpha = (M)0.70710678118654752440;  // 1/sqrt(2)
+    return mul_rn(mul_rn(a, (M)0.5), add_rn((M)1, erf_acc<M>(mul_rn(a, alpha))));
+  } else if constexpr (ACT == CEA_ACT_GELU_TANH) {
+    const M beta = (M)0.79788456080286535588;   // sqrt(2/pi)
+    const M kappa = (M)0.044715;
+    const M cube = mul_rn(mul_rn(a, a), a);
+    const M inner = mul_rn(beta, add_rn(a, mul_rn(kappa, cube)));
+    return mul_rn(mul_rn((M)0.5, a), add_rn((M)1, tanh_acc<M>(inner)));
+  } else {
+    return a <= (M)0 ? (M)0 : a;
+  }
+}
+
+template <typename T, int VEC, int ACT>
+__global__ __launch_bounds__(256) void gated_mul_kernel(const T* __restrict__ g, int64_t gs,
+                                                        const T* __restrict__ u, int64_t us,
+                                                        T* __restrict__ out, int64_t os,
+                                                        int64_t N, int I) {
   // grid: x over VEC-wide chunks of a row, y over rows (strided when N exceeds the grid)
   typedef typename math_of<T>::type M;
   const int c = (int)(blockIdx.x * 256 + threadIdx.x) * VEC;
@@ -561,9 +592,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ g, 
     load_vec<T, VEC>(u + row * us + c, uv);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const M a = widen<T, M>(gv[e]);
-      const M sl = rnd<T, M>(div_rn(a, add_rn((M)1, exp_acc(-a))));
-      ov[e] = narrow<T, M>(mul_rn(sl, widen<T, M>(uv[e])));
+      const M act = rnd<T, M>(gate_act<ACT, M>(widen<T, M>(gv[e])));
+      ov[e] = narrow<T, M>(mul_rn(act, widen<T, M>(uv[e])));
     }
     store_vec_stream<T, VEC>(out + row * os + c, ov);
   }
@@ -789,9 +819,9 @@ int launch_rmsnorm_rope(const cea_tensor* x, const cea_tensor* w, double eps,
   return CEA_EUNSUPPORTED;
 }
 
-template <typename T>
-static int silu_mul_typed(const cea_tensor* g, const cea_tensor* u, cea_tensor* o,
-                          hipStream_t st) {
+template <typename T, int ACT>
+static int gated_mul_typed(const cea_tensor* g, const cea_tensor* u, cea_tensor* o,
+                           hipStream_t st) {
   const int64_t N = g->size[0];
   const int I = (int)g->size[1];
   constexpr int V = 16 / sizeof(T);
@@ -801,25 +831,39 @@ static int silu_mul_typed(const cea_tensor* g, const cea_tensor* u, cea_tensor* 
   if (N == 0 || I / vw == 0) return CEA_OK;
   const dim3 grid((unsigned)((I / vw + 255) / 256), (unsigned)(N < 65535 ? N : 65535));
   if (vec)
-    hipLaunchKernelGGL((silu_mul_kernel<T, V>), grid, dim3(256), 0, st,
+    hipLaunchKernelGGL((gated_mul_kernel<T, V, ACT>), grid, dim3(256), 0, st,
                        (const T*)g->data, g->stride[0], (const T*)u->data, u->stride[0],
                        (T*)o->data, o->stride[0], N, I);
   else
-    hipLaunchKernelGGL((silu_mul_kernel<T, 1>), grid, dim3(256), 0, st,
+    hipLaunchKernelGGL((gated_mul_kernel<T, 1, ACT>), grid, dim3(256), 0, st,
                        (const T*)g->data, g->stride[0], (const T*)u->data, u->stride[0],
                        (T*)o->data, o->stride[0], N, I);
-  CEA_CHECK_LAUNCH("silu_mul");
+  CEA_CHECK_LAUNCH("gated_mul");
   return CEA_OK;
 }
 
-int launch_silu_mul(const cea_tensor* g, const cea_tensor* u, cea_tensor* o, hipStream_t st) {
-  switch (g->dtype) {
-    case CEA_BF16: return silu_mul_typed<bf16>(g, u, o, st);
-    case CEA_F16: return silu_mul_typed<f16>(g, u, o, st);
-    case CEA_F32: return silu_mul_typed<float>(g, u, o, st);
-    case CEA_F64: return silu_mul_typed<double>(g, u, o, st);
+template <typename T>
+static int gated_mul_act(const cea_tensor* g, const cea_tensor* u, cea_tensor* o, int act,
+                         hipStream_t st) {
+  switch (act) {
+    case CEA_ACT_SILU: return gated_mul_typed<T, CEA_ACT_SILU>(g, u, o, st);
+    case CEA_ACT_GELU: return gated_mul_typed<T, CEA_ACT_GELU>(g, u, o, st);
+    case CEA_ACT_GELU_TANH: return gated_mul_typed<T, CEA_ACT_GELU_TANH>(g, u, o, st);
+    case CEA_ACT_RELU: return gated_mul_typed<T, CEA_ACT_RELU>(g, u, o, st);
   }
-  set_error("silu_mul: unsupported dtype %s", dtype_name(g->dtype));
+  set_error("gated_mul: unknown activation %d", act);
+  return CEA_EUNSUPPORTED;
+}
+
+int launch_gated_mul(const cea_tensor* g, const cea_tensor* u, cea_tensor* o, int act,
+                     hipStream_t st) {
+  switch (g->dtype) {
+    case CEA_BF16: return gated_mul_act<bf16>(g, u, o, act, st);
+    case CEA_F16: return gated_mul_act<f16>(g, u, o, act, st);
+    case CEA_F32: return gated_mul_act<float>(g, u, o, act, st);
+    case CEA_F64: return gated_mul_act<double>(g, u, o, act, st);
+  }
+  set_error("gated_mul: unsupported dtype %s", dtype_name(g->dtype));
   return CEA_EUNSUPPORTED;
 }
 

@@ -5,7 +5,8 @@ collab_infer/models/llama.py.
 * :class:`RotaryEmbedding` - llama.py:64-77 (cos/sin at explicit positions, computed once per
   pass), with :func:`rope_inv_freq` from models/config.py:165-189
 * :func:`apply_rotary` - llama.py:80-88 (half-split rotation)
-* :func:`silu_mul` - ``act(gate) * up`` with ``act = F.silu`` (llama.py:45, 305, 316)
+* :func:`gated_mul` / :func:`silu_mul` - ``act(gate) * up`` for every activation of the
+  reference's ``_ACTIVATIONS`` (silu, gelu, gelu_pytorch_tanh, relu; llama.py:44-49, 305, 316)
 * :func:`rmsnorm_rope` - RMSNorm, rotary tables and rotation fused into one pass
 
 Each kernel reproduces the rounding points of the reference's separate tensor ops, so in
@@ -168,34 +169,59 @@ def rmsnorm_rope(x: torch.Tensor, weight: torch.Tensor, eps: float, positions: t
     return out.view(1, S, num_heads, C // num_heads)
 
 
-def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
-    """``F.silu(gate) * up`` (llama.py:305), gate/up may be column halves of one GEMM output."""
+# the reference's activation names (llama.py:44-49) -> CEA_ACT_* codes of cea_gated_mul
+ACTIVATION_CODES = {"silu": 0, "gelu": 1, "gelu_pytorch_tanh": 2, "relu": 3}
+
+
+def gated_mul(gate: torch.Tensor, up: torch.Tensor, act: str = "silu") -> torch.Tensor:
+    """``act(gate) * up`` (llama.py:44-49, 305) with ``act`` one of the reference's
+    activations; ``gate``/``up`` may be column halves of one fused GEMM output."""
+    if act not in ACTIVATION_CODES:
+        raise NotImplementedError(f"activation {act!r} is not supported")
     nat.require_device(gate, up)
     if gate.shape != up.shape:
         raise ValueError(f"gate {tuple(gate.shape)} and up {tuple(up.shape)} differ")
     g2, u2 = _rows(gate), _rows(up)
     out = torch.empty(g2.shape, dtype=gate.dtype, device=gate.device)
     a = [nat.tensor_arg(t) for t in (g2, u2, out)]
-    rc = nat.load_library().cea_silu_mul(*(byref(t) for t in a), nat.stream_of(gate.device))
-    nat.check(rc, "silu_mul")
+    rc = nat.load_library().cea_gated_mul(*(byref(t) for t in a), ACTIVATION_CODES[act],
+                                          nat.stream_of(gate.device))
+    nat.check(rc, "gated_mul")
     return out.view(gate.shape)
 
 
-_ACTIVATIONS_FUSED = {"silu": silu_mul}
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``F.silu(gate) * up`` (llama.py:305)."""
+    return gated_mul(gate, up, "silu")
+
+
+class _GatedActivation:
+    """``act(gate) * up`` for one activation name, as one kernel."""
+
+    def __init__(self, name: str) -> None:
+        self.name = name
+
+    def __call__(self, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+        return gated_mul(gate, up, self.name)
+
+    def __repr__(self) -> str:
+        return f"gated_activation({self.name!r})"
 
 
 def gated_activation(name: str):
     """The fused ``act(gate) * up`` for a model's ``hidden_act`` (llama.py:44-49, 298)."""
-    if name not in _ACTIVATIONS_FUSED:
+    if name not in ACTIVATION_CODES:
         raise NotImplementedError(f"activation {name!r} is not supported")
-    return _ACTIVATIONS_FUSED[name]
+    return _GatedActivation(name)
 
 
 __all__ = [
+    "ACTIVATION_CODES",
     "RMSNorm",
     "RotaryEmbedding",
     "apply_rotary",
     "gated_activation",
+    "gated_mul",
     "rmsnorm",
     "rmsnorm_rope",
     "rope_inv_freq",

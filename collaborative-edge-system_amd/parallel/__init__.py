@@ -1,0 +1,10 @@
+"""The import paths of ``collab_infer.parallel`` for this path's functions.
+
+``<pkg>.parallel.attention``, ``<pkg>.parallel.sequence_parallel`` and
+``<pkg>.parallel.partition`` export the reference modules' public names
+(collab_infer/parallel/attention.py:304-315, sequence_parallel.py:283-292,
+partition.py:247-254) with the reference's signatures, so code written against
+``collab_infer.parallel.<module>`` switches by changing the package name.
+"""
+
+from . import attention, partition, sequence_parallel  # noqa: F401

@@ -105,6 +105,13 @@ class LocalGroup:
         w = self.to_wire(t)
         return t if w is t else w.to(t.dtype)
 
+    def gathered(self, key: str, local: torch.Tensor, compress: bool = False) -> List[torch.Tensor]:
+        """What a collective delivers to this rank, in rank order: its own tensor ``local``
+        and every other rank's tensor registered under ``key``.  A compressed transfer sends
+        every piece, the rank's own included, through the wire dtype (comm.py:484-486)."""
+        out = [local if r == self.rank else self.shard(r)[key] for r in range(self.size)]
+        return [self.received(t) for t in out] if compress else out
+
 
 def _kv_from(comm: LocalGroup, src: int, own: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]):
     """The KV block of rank ``src`` as the ring delivers it: received blocks went through
@@ -280,6 +287,13 @@ def partitioned_attention(
     return result[0] if len(result) == 1 else tuple(result)
 
 
+def _dkv_partitions(comm: LocalGroup, own):
+    """Every rank's KV partition in rank order (the all-gather order).  Each rank attends to
+    the partition it stores at full precision; only the f32 (out | lse) message crosses the
+    wire, uncompressed (sequence_parallel.py:270-279)."""
+    return [own if i == comm.rank else _raw_kv(comm, i) for i in range(comm.size)]
+
+
 def distributed_kv_attention(
     q: torch.Tensor,
     k_local: torch.Tensor,
@@ -292,39 +306,51 @@ def distributed_kv_attention(
     scale: Optional[float] = None,
     kv_map: KVMap = None,
     kv_block: Optional[int] = None,
-    wire: bool = False,
 ) -> torch.Tensor:
     """A replicated query against a KV cache sharded over the ranks of ``comm``
     (sequence_parallel.py:250-280); returns ``[B, Sq, Hq, D]`` in ``q.dtype``.
 
-    By default every rank's partition runs in one split-KV launch with the merge in its
-    reduction.  ``wire=True`` runs the multi-device data flow instead: each rank's partial
-    ``(out, lse)`` is packed into its slot of the all-gathered ``[n, B, Sq, H, D+1]`` buffer
-    (the message layout of sequence_parallel.py:275-276) and the buffer is merged in place
-    (:277-280)."""
+    Every rank's partition runs in one split-KV launch, the exact merge in its reduction;
+    :func:`distributed_kv_attention_packed` runs the multi-device message flow instead."""
     if comm.size == 1:
         o, _ = attention_with_lse(q, k_local, v_local, q_pos, k_pos_local, causal=causal,
                                   scale=scale, kv_map=kv_map, kv_block=kv_block)
         return o.to(q.dtype)
-    # every rank attends to the partition it stores at full precision; only the f32
-    # (out | lse) message crosses the wire, uncompressed (sequence_parallel.py:270-279)
-    own = (k_local, v_local, k_pos_local)
-    parts = [own if i == comm.rank else _raw_kv(comm, i) for i in range(comm.size)]
-    if wire:
-        B, Sq, Hq, D = q.shape
-        gathered = torch.empty(comm.size, B, Sq, Hq, D + 1, dtype=accumulation_dtype(q.dtype),
-                               device=q.device)
-        for i, (kk, vv, pp) in enumerate(parts):
-            o, l = attention_with_lse(q, kk, vv, q_pos, pp, causal=causal, scale=scale,
-                                      kv_map=kv_map, kv_block=kv_block)
-            pack_partial(o, l, gathered[i])
-        return merge_packed(gathered, out_dtype=q.dtype)
+    parts = _dkv_partitions(comm, (k_local, v_local, k_pos_local))
     if kv_block is not None:
         partial = [attention_with_lse(q, kk, vv, q_pos, pp, causal=causal, scale=scale,
                                       kv_map=kv_map, kv_block=kv_block) for kk, vv, pp in parts]
         o, _ = merge_attention_list([p[0] for p in partial], [p[1] for p in partial])
         return o.to(q.dtype)
     return partitioned_attention(q, q_pos, parts, causal=causal, scale=scale, kv_map=kv_map)
+
+
+def distributed_kv_attention_packed(
+    q: torch.Tensor,
+    k_local: torch.Tensor,
+    v_local: torch.Tensor,
+    q_pos: torch.Tensor,
+    k_pos_local: torch.Tensor,
+    comm: LocalGroup,
+    *,
+    causal: bool = True,
+    scale: Optional[float] = None,
+    kv_map: KVMap = None,
+    kv_block: Optional[int] = None,
+) -> torch.Tensor:
+    """:func:`distributed_kv_attention` through the data flow of the multi-device version:
+    each rank's partial ``(out, lse)`` is packed into its slot of the all-gathered
+    ``[n, B, Sq, H, D+1]`` buffer (the message layout of sequence_parallel.py:275-276) and
+    the buffer is merged in place, cast to ``q.dtype`` (:277-280)."""
+    parts = _dkv_partitions(comm, (k_local, v_local, k_pos_local))
+    B, Sq, Hq, D = q.shape
+    gathered = torch.empty(comm.size, B, Sq, Hq, D + 1, dtype=accumulation_dtype(q.dtype),
+                           device=q.device)
+    for i, (kk, vv, pp) in enumerate(parts):
+        o, l = attention_with_lse(q, kk, vv, q_pos, pp, causal=causal, scale=scale,
+                                  kv_map=kv_map, kv_block=kv_block)
+        pack_partial(o, l, gathered[i])
+    return merge_packed(gathered, out_dtype=q.dtype)
 
 
 # --------------------------------------------------------------------------------------
@@ -388,28 +414,58 @@ def ulysses_scatter(q, k, v, positions, comm: LocalGroup, seq_sizes: Sequence[in
     return q_f, k_f, v_f, pos_f
 
 
-def ulysses_gather(out_heads_of_ranks: Sequence[torch.Tensor], comm: LocalGroup,
-                   seq_sizes: Sequence[int], head_shards: Sequence[HeadShard]) -> torch.Tensor:
-    """Head-sharded -> sequence-sharded (sequence_parallel.py:182-194).  On one GPU every
-    rank's head output ``[B, S, h_j, D]`` is available; returns this rank's tokens with all
-    heads ``[B, s_r, H, D]``, built by one kernel (``cea_ulysses_gather``)."""
-    r = comm.rank
-    outs = list(out_heads_of_ranks)
-    if len(outs) != comm.size:
-        raise ValueError("need one head output per rank")
-    if comm.size > 1:
-        outs = [comm.received(o) for o in outs]
+def _head_concat(outs: Sequence[torch.Tensor], start: int, length: int) -> torch.Tensor:
+    """Tokens ``[start, start + length)`` of every part ``[B, S, h_j, D]``, heads
+    concatenated in part order, by one kernel (``cea_ulysses_gather``)."""
     outs = [_heads_contiguous(o) for o in outs]
     nat.require_device(*outs)
-    start = offsets_of(seq_sizes)[r]
     B, _, _, D = outs[0].shape
     H = sum(o.shape[2] for o in outs)
-    res = torch.empty(B, seq_sizes[r], H, D, dtype=outs[0].dtype, device=outs[0].device)
+    res = torch.empty(B, length, H, D, dtype=outs[0].dtype, device=outs[0].device)
     lib = nat.load_library()
     oa, ra = nat.tensor_array(outs), nat.tensor_arg(res)
     rc = lib.cea_ulysses_gather(len(outs), oa, int(start), byref(ra), nat.stream_of(res.device))
     nat.check(rc, "ulysses_gather")
     return res
+
+
+def ulysses_gather(out_heads: torch.Tensor, comm: LocalGroup, seq_sizes: Sequence[int],
+                   head_shards: Sequence[HeadShard]) -> torch.Tensor:
+    """Second Ulysses all-to-all: head-sharded ``[B, S, h_r, D]`` -> ``[B, s_r, H, D]``
+    (sequence_parallel.py:182-194).
+
+    ``out_heads`` is this rank's head output over the whole sequence; the other simulated
+    ranks' head outputs are read where they are registered in ``comm`` (``out_heads`` of
+    each rank's shard), rounded through the wire dtype as the compressed all-to-all does.
+    One kernel writes this rank's tokens with all heads."""
+    n, r = comm.size, comm.rank
+    if len(seq_sizes) != n:
+        raise ValueError(f"seq_sizes {list(seq_sizes)} do not match a group of {n}")
+    if len(head_shards) != n:
+        raise ValueError("need one head shard per rank")
+    outs = comm.gathered("out_heads", out_heads, compress=n > 1)
+    for j, o in enumerate(outs):
+        if o.shape[2] != head_shards[j].q_count:
+            raise ValueError(f"rank {j} sent {o.shape[2]} heads, its shard has {head_shards[j].q_count}")
+    return _head_concat(outs, offsets_of(seq_sizes)[r], seq_sizes[r])
+
+
+def gather_heads(out_local: torch.Tensor, comm: LocalGroup,
+                 head_shards: Sequence[HeadShard]) -> torch.Tensor:
+    """All-gather of per-rank head slices ``[B, S, h_r, D]`` into ``[B, S, H, D]``
+    (sequence_parallel.py:242-247, uncompressed): the other simulated ranks' slices are read
+    where they are registered in ``comm`` (``out_heads``), and one kernel concatenates the
+    heads in rank order."""
+    if len(head_shards) != comm.size:
+        raise ValueError("need one head shard per rank")
+    if comm.size == 1:
+        return out_local
+    outs = comm.gathered("out_heads", out_local)
+    S = out_local.shape[1]
+    for j, o in enumerate(outs):
+        if o.shape[2] != head_shards[j].q_count or o.shape[1] != S:
+            raise ValueError(f"rank {j}'s slice {tuple(o.shape)} does not match its head shard")
+    return _head_concat(outs, 0, S)
 
 
 def ulysses_attention(
@@ -431,7 +487,7 @@ def ulysses_attention(
     Every simulated rank's head-sharded local attention runs here (the gather needs all of
     them); returns ``(out [B, s_r, Hq, D], (k_heads, v_heads, pos_full))`` for this rank.
     """
-    outs = []
+    out_mine = None
     mine = None
     for j in range(comm.size):
         cj = comm.view_as(j)
@@ -450,16 +506,24 @@ def ulysses_attention(
             pk, pv, pp = comm.shard(j)["past"]
             k_att, v_att, p_att = (torch.cat([pk, k_f], 1), torch.cat([pv, v_f], 1),
                                    torch.cat([pp, pos_f], 1))
-        outs.append(attention(q_f, k_att, v_att, pos_f, p_att, causal=causal, scale=scale,
-                              kv_map=head_shards[j].kv_map, kv_block=kv_block))
+        o = attention(q_f, k_att, v_att, pos_f, p_att, causal=causal, scale=scale,
+                      kv_map=head_shards[j].kv_map, kv_block=kv_block)
         if j == comm.rank:
+            out_mine = o
             mine = (k_f.contiguous(), v_f.contiguous(), pos_f)
-    return ulysses_gather(outs, comm, seq_sizes, head_shards), mine
+        else:  # what rank j sends back in the second all-to-all
+            comm.set_shard(j, out_heads=o)
+    return ulysses_gather(out_mine, comm, seq_sizes, head_shards), mine
 
 
-def gather_sequence(x_parts: Sequence[torch.Tensor], layout: SequenceLayout, dim: int = 1) -> torch.Tensor:
-    """Reassemble per-rank sequence shards in global token order (sequence_parallel.py:55-62)."""
-    return layout.unshard(list(x_parts), dim=dim)
+def gather_sequence(x_local: torch.Tensor, layout: SequenceLayout, comm: LocalGroup,
+                    dim: int = 1) -> torch.Tensor:
+    """All-gather sequence shards and restore global token order (sequence_parallel.py:55-62).
+    The other simulated ranks' shards are read where they are registered in ``comm``
+    (``x`` of each rank's shard)."""
+    if comm.size == 1:
+        return x_local
+    return layout.unshard(comm.gathered("x", x_local), dim=dim)
 
 
 def shard_sequence(x: torch.Tensor, layout: SequenceLayout, rank: int, dim: int = 1) -> torch.Tensor:
@@ -470,6 +534,8 @@ def shard_sequence(x: torch.Tensor, layout: SequenceLayout, rank: int, dim: int 
 __all__ = [
     "LocalGroup",
     "distributed_kv_attention",
+    "distributed_kv_attention_packed",
+    "gather_heads",
     "gather_sequence",
     "partitioned_attention",
     "ring_attention",

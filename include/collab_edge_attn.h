@@ -44,6 +44,12 @@ extern "C" {
 #define CEA_MAX_PARTS 16      /* maximum number of partial results one merge call combines   */
 #define CEA_MAX_MAPPED_HEADS 512 /* maximum query heads when an explicit kv_map is given     */
 
+/* gated activations of cea_gated_mul: the reference's _ACTIVATIONS table (llama.py:44-49) */
+#define CEA_ACT_SILU 0        /* F.silu                              */
+#define CEA_ACT_GELU 1        /* F.gelu (erf form)                   */
+#define CEA_ACT_GELU_TANH 2   /* F.gelu(x, approximate="tanh")       */
+#define CEA_ACT_RELU 3        /* F.relu                              */
+
 typedef struct cea_tensor {
   void* data;                    /* device pointer to element [0, ..., 0]       */
   int32_t dtype;                 /* CEA_F32 / CEA_BF16 / CEA_F16 / CEA_F64 / CEA_I64 */
@@ -259,6 +265,15 @@ int cea_rmsnorm_rope(const cea_tensor* x, const cea_tensor* weight, double eps,
  *   out [N,I].
  */
 int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, void* stream);
+
+/*
+ * Gated activation: out = act(gate) * up with act(gate) rounded to the tensor dtype before
+ * the product, act one of CEA_ACT_* (silu, gelu, gelu_pytorch_tanh, relu).
+ * Replaces act(gate) * up for every entry of _ACTIVATIONS (collab_infer/models/llama.py:44-49,
+ * 298-305, 316).  Shapes as cea_silu_mul; an unknown act returns CEA_EUNSUPPORTED.
+ */
+int cea_gated_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, int32_t act,
+                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -81,6 +81,20 @@ def silu_gate(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return F.silu(gate) * up
 
 
+# llama.py:44-49 (_ACTIVATIONS)
+ACTIVATIONS = {
+    "silu": F.silu,
+    "gelu": F.gelu,
+    "gelu_pytorch_tanh": lambda x: F.gelu(x, approximate="tanh"),
+    "relu": F.relu,
+}
+
+
+def gated(gate: torch.Tensor, up: torch.Tensor, act: str) -> torch.Tensor:
+    """llama.py:305: self.act(gate) * up, two separately rounded tensor ops."""
+    return ACTIVATIONS[act](gate) * up
+
+
 def linear(x, weight, bias=None):
     """tensor_parallel.py:294-295: F.linear of the fused projection, in the input dtype on the
     CPU (f32 accumulation for bf16 / f16 inputs)."""

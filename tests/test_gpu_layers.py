@@ -184,6 +184,46 @@ def test_silu_mul_on_fused_gemm_halves(cea, dev):
     assert_close_layer(y, L.silu_gate(g, u), "silu halves")
 
 
+@pytest.mark.parametrize("act", ["gelu", "gelu_pytorch_tanh", "relu"])
+@pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (4096, 14336)), (torch.float16, (300, 2056)),
+                                         (torch.float32, (100, 3000)), (torch.float64, (10, 77))])
+def test_gated_activations(cea, dev, act, dtype, shape):
+    """gelu / gelu_pytorch_tanh / relu gates (llama.py:44-49, 305) against the oracle's
+    separately rounded torch ops; gate values spread over +-8 so the activations' tails and
+    the relu kink are exercised."""
+    g = (torch.randn(*shape, generator=_gen(20)) * 3).to(dtype)
+    u = torch.randn(*shape, generator=_gen(21)).to(dtype)
+    y = cea.layers.gated_mul(g.to(dev), u.to(dev), act)
+    y2 = cea.layers.gated_activation(act)(g.to(dev), u.to(dev))
+    torch.cuda.synchronize()
+    ref = L.gated(g, u, act)
+    assert torch.equal(y, y2)
+    if act == "relu" or dtype == torch.float64:
+        assert_close_layer(y, ref, f"{act} {dtype}")
+        return
+    # Both sides evaluate the GELU forms in f32 with different erf / tanh implementations
+    # (torch's vectorised CPU code differs from correctly rounded values in a third of the
+    # elements, by up to 1e-6 absolute and, in the negative tail where 1 + erf(x/sqrt 2) and
+    # 1 + tanh(.) cancel, 2e-5).  f32: the north-star tolerance, normwise rel <= 1e-5.  bf16 /
+    # f16: a last-bit flip of the rounded activation reaches the result scaled by |up|, so the
+    # bound is one ulp of the result + one ulp of the activation times |up| + 2e-5 |up|, and
+    # the abs bound 2e-2 holds wherever |result| < 2.
+    a, b, uu = y.cpu().double(), ref.double(), u.double().abs()
+    diff = (a - b).abs()
+    assert torch.isfinite(a).all()
+    if dtype == torch.float32:
+        rel = diff.max().item() / b.abs().max().item()
+        assert rel <= 1e-5, f"{act} f32: rel {rel:.3e}"
+        return
+    act_ref = L.ACTIVATIONS[act](g).double()
+    bound = (_ulp(b, dtype).double() + _ulp(act_ref, dtype).double() * uu) * 1.0001 + 2e-5 * uu
+    over = diff > bound
+    assert not over.any(), f"{act} {dtype}: {int(over.sum())} beyond the bound, max {diff.max().item():.3e}"
+    small = b.abs() < 2  # where one ulp of the result is below the abs bound
+    assert diff[small].max().item() <= 2e-2
+    assert (diff > 0).double().mean().item() <= 0.1
+
+
 def test_layer_errors(cea, dev):
     x = torch.randn(4, 100, device=dev)
     with pytest.raises(ValueError):
@@ -193,5 +233,7 @@ def test_layer_errors(cea, dev):
         cea.silu_mul(x, torch.randn(4, 99, device=dev))
     with pytest.raises(NotImplementedError):
         cea.layers.gated_activation("gelu_new")
+    with pytest.raises(NotImplementedError):
+        cea.layers.gated_mul(x, x, "swish")
     with pytest.raises(RuntimeError):
         cea.silu_mul(x.cpu(), x.cpu())  # host tensors are refused, never computed on the CPU

@@ -208,8 +208,8 @@ def test_distributed_kv_ignores_activation_wire_dtype(cea, dev, wire_kv):
         group.set_shard(r, k=parts[-1][0].to(dev), v=parts[-1][1].to(dev), pos=parts[-1][2].to(dev))
         start += n
     own = [t.to(dev) for t in parts[1]]
-    out = cea.distributed_kv_attention(q.to(dev), own[0], own[1], qpos.to(dev), own[2], group,
-                                       wire=wire_kv)
+    fn = cea.distributed_kv_attention_packed if wire_kv else cea.distributed_kv_attention
+    out = fn(q.to(dev), own[0], own[1], qpos.to(dev), own[2], group)
     ro = sp_ref.distributed_kv_share(q, qpos, parts)
     torch.cuda.synchronize()
     assert out.dtype == torch.float64

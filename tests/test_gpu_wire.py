@@ -59,7 +59,10 @@ def test_ulysses_scatter_gather_match_oracle(cea, dev, dtype, world, weights, ki
         outs.append(got[0] * 2)  # any per-rank head output: the scattered queries, doubled
         outs_ref.append(want[0] * 2)
     for r in range(world):
-        got = cea.ulysses_gather(outs, _group(cea, shards_d, r), layout.sizes, heads)
+        grp = _group(cea, shards_d, r)
+        for j in range(world):  # what the other ranks send back in the second all-to-all
+            grp.set_shard(j, out_heads=outs[j])
+        got = cea.ulysses_gather(outs[r], grp, layout.sizes, heads)
         want = sp_ref.ulysses_gather(outs_ref, layout.sizes, r)
         torch.cuda.synchronize()
         assert torch.equal(got.cpu(), want), f"gather rank {r}"
@@ -149,8 +152,17 @@ def test_ulysses_workload_full_size(cea, dev):
     assert torch.equal(pos_f, pos)
     outs = [q[:, :, h.q_start:h.q_start + h.q_count] for h in heads]
     for r in (0, 5):
-        got = cea.ulysses_gather(outs, _group(cea, shards, r), layout.sizes, heads)
+        grp = _group(cea, shards, r)
+        for j, o in enumerate(outs):
+            grp.set_shard(j, out_heads=o)
+        got = cea.ulysses_gather(outs[r], grp, layout.sizes, heads)
         assert torch.equal(got, shards[r][0])
+    # the head gather of Ulysses decoding (sequence_parallel.py:242-247): every rank's head
+    # slice over the same tokens, concatenated along the heads
+    grp = _group(cea, shards, 3)
+    for j, o in enumerate(outs):
+        grp.set_shard(j, out_heads=o)
+    assert torch.equal(cea.gather_heads(outs[3], grp, heads), q)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=str)
@@ -201,7 +213,7 @@ def test_kv_decode_packed_route_matches_fused(cea, dev):
     for r, (k, v, p) in enumerate(parts):
         group.set_shard(r, k=k, v=v, pos=p)
     fused = cea.distributed_kv_attention(w.q, *parts[0][:2], w.q_pos, parts[0][2], group)
-    packed = cea.distributed_kv_attention(w.q, *parts[0][:2], w.q_pos, parts[0][2], group, wire=True)
+    packed = cea.distributed_kv_attention_packed(w.q, *parts[0][:2], w.q_pos, parts[0][2], group)
     torch.cuda.synchronize()
     assert packed.dtype == torch.bfloat16 and packed.shape == fused.shape
     assert (packed.float() - fused.float()).abs().max().item() <= 2e-2

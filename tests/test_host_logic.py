@@ -351,3 +351,20 @@ def test_ring_attention_rejects_nonpositive_kv_block(cea):
             cea.ring_attention(q, kv, kv, pos, pos, group, [4, 4], kv_block=bad)
         with pytest.raises(ValueError):
             cea.attention_with_lse(q, kv, kv, pos, pos, kv_block=bad)
+
+
+@pytest.mark.parametrize("kind", ["contiguous", "zigzag"])
+def test_gather_sequence_restores_global_order(cea, kind):
+    """gather_sequence(x_local, layout, comm, dim) (sequence_parallel.py:55-62): the other
+    simulated ranks' shards, registered as ``x``, all-gathered and put back in token order."""
+    S, world = 23, 3
+    x = torch.arange(2 * S * 5).view(2, S, 5)
+    layout = cea.SequenceLayout(S, world, [3, 1, 2], kind)
+    group = cea.LocalGroup(world)
+    for r in range(world):
+        group.set_shard(r, x=layout.shard(x, r))
+    for r in range(world):
+        got = cea.gather_sequence(layout.shard(x, r), layout, group.view_as(r), dim=1)
+        assert torch.equal(got, x)
+    single = cea.LocalGroup(1)
+    assert cea.gather_sequence(x, cea.SequenceLayout(S, 1), single) is x

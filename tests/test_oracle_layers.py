@@ -217,6 +217,85 @@ def test_planted_missing_gate_factor_is_caught(monkeypatch):
         test_silu_gate_f64_closed_form()
 
 
+# ---- the other gated activations (llama.py:44-49) ---------------------------------------------
+
+_ERF = np.vectorize(math.erf)
+
+
+def _act_closed(name: str, g: np.ndarray) -> np.ndarray:
+    """The activations from their definitions, in f64 (independent of torch)."""
+    if name == "silu":
+        return g / (1 + np.exp(-g))
+    if name == "gelu":  # g * Phi(g), Phi the standard normal CDF
+        return g * 0.5 * (1 + _ERF(g / math.sqrt(2.0)))
+    if name == "gelu_pytorch_tanh":  # the tanh approximation of Hendrycks & Gimpel (2016)
+        return 0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g ** 3)))
+    if name == "relu":
+        return np.maximum(g, 0.0)
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name", ["silu", "gelu", "gelu_pytorch_tanh", "relu"])
+def test_gated_activation_f64_closed_form(name):
+    g = torch.randn(64, 300, generator=_gen(16), dtype=torch.float64) * 4
+    u = torch.randn(64, 300, generator=_gen(17), dtype=torch.float64)
+    want = _act_closed(name, g.numpy()) * u.numpy()
+    assert np.abs(L.gated(g, u, name).numpy() - want).max() <= 1e-12
+
+
+_F32 = np.float32
+_ERF32 = np.vectorize(lambda v: _F32(math.erf(float(v))), otypes=[np.float32])
+_TANH32 = np.vectorize(lambda v: _F32(math.tanh(float(v))), otypes=[np.float32])
+
+
+def _act_f32(name: str, g: np.ndarray) -> np.ndarray:
+    """The activation formulas evaluated in f32 arithmetic (torch's op math for bf16), with
+    correctly rounded erf / tanh; returned as f64."""
+    g = g.astype(np.float32)
+    if name == "gelu":
+        r = (g * _F32(0.5)) * (_F32(1) + _ERF32(g * _F32(0.70710678118654752440)))
+    elif name == "gelu_pytorch_tanh":
+        inner = _F32(0.79788456080286535588) * (g + _F32(0.044715) * (g * g * g))
+        r = (_F32(0.5) * g) * (_F32(1) + _TANH32(inner))
+    else:
+        r = np.maximum(g, _F32(0))
+    return r.astype(np.float64)
+
+
+@pytest.mark.parametrize("name", ["gelu", "gelu_pytorch_tanh", "relu"])
+def test_gated_activation_bf16_rounding_points(name):
+    """act(gate) rounded to bf16, then the product rounded (llama.py:305).  The activation
+    is computed in f32; where 1 + erf / 1 + tanh cancels (the negative tail) torch's CPU
+    erf / tanh differ from correctly rounded ones by up to 2e-5 absolute, scaled by |up|."""
+    g = (torch.randn(512, 1024, generator=_gen(18)) * 3).to(torch.bfloat16)
+    u = torch.randn(512, 1024, generator=_gen(19)).to(torch.bfloat16)
+    gn, un = g.double().numpy(), u.double().numpy()
+    want = bf16_round(bf16_round(_act_f32(name, gn)) * un)
+    y = L.gated(g, u, name).double().numpy()
+    diff = np.abs(y - want)
+    assert (diff <= ulp_bf16(want) * 1.0001 + 2e-5 * np.abs(un)).all()
+    assert (diff > 0).mean() <= 0.05
+    if name == "relu":
+        assert (diff == 0).all()
+    # a single fused rounding of act * up misses the first rounding point in many elements
+    fused = bf16_round(_act_f32(name, gn) * un)
+    if name != "relu":
+        assert (np.abs(fused - want) > 0).mean() > 0.05
+
+
+def test_gelu_planted_mistakes_are_caught(monkeypatch):
+    """The two GELU forms differ by up to ~5e-4, far above the f64 pins: swapping them, or
+    dropping the cubic term of the tanh form, fails the closed-form check."""
+    tanh_form = L.ACTIVATIONS["gelu_pytorch_tanh"]
+    monkeypatch.setitem(L.ACTIVATIONS, "gelu", tanh_form)
+    with pytest.raises(AssertionError):
+        test_gated_activation_f64_closed_form("gelu")
+    monkeypatch.setitem(L.ACTIVATIONS, "gelu_pytorch_tanh",
+                        lambda x: 0.5 * x * (1 + torch.tanh(math.sqrt(2 / math.pi) * x)))
+    with pytest.raises(AssertionError):
+        test_gated_activation_f64_closed_form("gelu_pytorch_tanh")
+
+
 def test_rmsnorm_rope_f64_composition():
     S, H, D = 17, 4, 32
     x = torch.randn(S, H * D, generator=_gen(10), dtype=torch.float64)
