@@ -59,6 +59,11 @@ _SIGNATURES = {
          ctypes.c_int32, _P, _P, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t,
          ctypes.c_void_p],
     ),
+    "cea_attention_with_lse_noalloc": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_double, ctypes.POINTER(ctypes.c_int32),
+         ctypes.c_int32, _P, _P, ctypes.c_int32, ctypes.c_void_p],
+    ),
     "cea_attention_merge_final": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_double, ctypes.POINTER(ctypes.c_int32),

@@ -4,6 +4,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "cea_kernels.hpp"
 
 namespace cea {
@@ -250,6 +253,45 @@ static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t s
   return launch_attn_generic(p, st);
 }
 
+// ---- scratch of the no-allocation entry point -------------------------------------------
+// A file-scope device array replaces the caller's workspace for callers that cannot allocate
+// (code under graph capture, tight serving loops).  Every GPU holds its own copy at its own
+// address until the process ends; host code never uses the array's name as a device address,
+// only the per-device pointer that hipGetSymbolAddress returns.  Calls that overlap on one GPU
+// share (and race on) this memory.
+static __device__ __align__(256) char scratch[CEA_NOALLOC_SCRATCH_BYTES];
+
+static constexpr int kMaxDevices = 64;
+static std::atomic<char*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The device address of this GPU's scratch, looked up once per device (with that device
+// current) on its first use.
+static int device_scratch(char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "no-alloc scratch: hipGetDevice failed: %s",
+              hipGetErrorString(e));
+  CEA_REQUIRE(dev >= 0 && dev < kMaxDevices, CEA_EUNSUPPORTED,
+              "no-alloc scratch: device %d beyond the %d supported", dev, kMaxDevices);
+  char* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      CEA_REQUIRE(e == hipSuccess && addr != nullptr, CEA_ELAUNCH,
+                  "no-alloc scratch: hipGetSymbolAddress failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+      ptr = (char*)addr;
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return CEA_OK;
+}
+
 }  // namespace cea
 
 using namespace cea;
@@ -282,6 +324,26 @@ int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_t
                             lse, accumulate);
   if (rc) return rc;
   return run_attention(p, (char*)workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int cea_attention_with_lse_noalloc(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
+                                   const cea_tensor* q_pos, const cea_tensor* k_pos,
+                                   int32_t causal, double scale, const int32_t* kv_map,
+                                   int32_t kv_map_len, cea_tensor* out, cea_tensor* lse,
+                                   int32_t accumulate, void* stream) {
+  AttnParams p;
+  int rc = make_attn_params(&p, q, k, v, q_pos, k_pos, causal, scale, kv_map, kv_map_len, out,
+                            lse, accumulate);
+  if (rc) return rc;
+  const size_t need = cea_attention_workspace_bytes(p.B, p.Sq, p.Hq, p.Sk, p.Hkv, p.D,
+                                                    p.in_dtype);
+  CEA_REQUIRE(need <= (size_t)CEA_NOALLOC_SCRATCH_BYTES, CEA_ENOSPACE,
+              "attention_with_lse_noalloc: this call needs %zu bytes of scratch, the static "
+              "scratch holds %zu (use cea_attention_with_lse with a workspace)",
+              need, (size_t)CEA_NOALLOC_SCRATCH_BYTES);
+  char* ws = nullptr;
+  if ((rc = device_scratch(&ws))) return rc;
+  return run_attention(p, ws, (size_t)CEA_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
 }
 
 static int merge_impl(int32_t n, const cea_tensor* outs, const cea_tensor* lses, cea_tensor* out,

@@ -44,6 +44,8 @@ extern "C" {
 #define CEA_MAX_PARTS 16      /* maximum number of partial results one merge call combines   */
 #define CEA_MAX_MAPPED_HEADS 512 /* maximum query heads when an explicit kv_map is given     */
 
+#define CEA_NOALLOC_SCRATCH_BYTES (32 << 20) /* per-GPU scratch of cea_attention_with_lse_noalloc */
+
 /* gated activations of cea_gated_mul: the reference's _ACTIVATIONS table (llama.py:44-49) */
 #define CEA_ACT_SILU 0        /* F.silu                              */
 #define CEA_ACT_GELU 1        /* F.gelu (erf form)                   */
@@ -95,6 +97,23 @@ int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_t
                            double scale, const int32_t* kv_map, int32_t kv_map_len,
                            cea_tensor* out, cea_tensor* lse, int32_t accumulate,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * cea_attention_with_lse without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference: it computes exactly what cea_attention_with_lse computes,
+ * with the same kernels, but its scratch (tile summaries or split-KV chunk partials) is a
+ * static device array of CEA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.  It
+ * calls no allocating routine; a call whose scratch need (cea_attention_workspace_bytes)
+ * exceeds the array returns CEA_ENOSPACE.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race and must be serialised
+ * by the caller.
+ */
+int cea_attention_with_lse_noalloc(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
+                                   const cea_tensor* q_pos, const cea_tensor* k_pos,
+                                   int32_t causal, double scale, const int32_t* kv_map,
+                                   int32_t kv_map_len, cea_tensor* out, cea_tensor* lse,
+                                   int32_t accumulate, void* stream);
 
 /*
  * The last step of a ring: merges attention over one more KV block into the running
