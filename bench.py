@@ -237,16 +237,34 @@ def bench_wire(cea, torch, steps, warmup, dev):
     return res
 
 
+def _event_timed(fn, steps: int, warmup: int, torch, dev):
+    """(wall seconds per call, GPU milliseconds per call from two HIP events on the launch
+    stream around the same timed calls)."""
+    for _ in range(warmup):
+        fn()
+    stream = torch.cuda.current_stream(dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    a.record(stream)
+    for _ in range(steps):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps, a.elapsed_time(b) / steps
+
+
 def bench_ulysses(cea, torch, steps, warmup, dev):
     w = cea.workloads.ulysses_share(device=dev)
 
     def step():
         return cea.attention_with_lse(w.q, w.k, w.v, w.pos, w.pos, kv_map=w.kv_map)
 
-    sec = _timed(step, steps, warmup, torch)
+    sec, gpu_ms = _event_timed(step, steps, warmup, torch, dev)
     tf = w.flop / sec / 1e12
     return {"value": round(tf, 1), "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-            "ms_per_step": round(sec * 1e3, 4), "flop": w.flop, "valid_tokens": w.valid,
+            "ms_per_step": round(sec * 1e3, 4), "gpu_ms_per_step": round(gpu_ms, 4),
+            "flop": w.flop, "valid_tokens": w.valid,
             "workload": "Ulysses sp=8 share: 65536 tokens, 8/2 heads, D=128, bf16, causal, "
                         "4 packed sequences + right padding, emits f32 lse"}
 
