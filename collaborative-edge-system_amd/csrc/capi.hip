@@ -241,6 +241,7 @@ static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t s
                          bool allow_decode = true) {
   if (allow_decode && p.Sk > 0 && use_decode(p))
     return run_decode(&p, 1, nullptr, nullptr, ws, ws_bytes, st);
+  if (p.Sk > 0 && f32_mfma_supported(p)) return launch_attn_f32_mfma(p, st);
   if (p.Sk > 0 && prefill_mfma_supported(p)) {
     const size_t need = tile_bytes(p.B, p.Sk);
     CEA_REQUIRE(ws != nullptr && ws_bytes >= need, CEA_ENOSPACE,

@@ -159,6 +159,8 @@ int launch_tile_info(const int64_t* k_pos, int64_t kps_b, int64_t kps_s, int32_t
                      TileInfo* tiles, int32_t ntiles, hipStream_t s);
 bool prefill_mfma_supported(const AttnParams& p);
 int launch_attn_prefill_mfma(const AttnParams& p, hipStream_t s);
+bool f32_mfma_supported(const AttnParams& p);
+int launch_attn_f32_mfma(const AttnParams& p, hipStream_t s);
 bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype,
                       const HeadMap& map);
 constexpr int kDecodeMaxChunks = 1024;  // key chunks per (batch, kv head), all partitions

@@ -215,3 +215,43 @@ def test_ring_attention_fused_cast_is_exact(cea, dev):
     torch.cuda.synchronize()
     assert res.dtype == torch.bfloat16
     assert torch.equal(res, o.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_f32_matrix_core_and_generic_paths(cea, dev, D):
+    """f32 inputs with 16-byte aligned rows run the f32 matrix-core kernel; a view whose rows
+    start 4 bytes off alignment runs the generic kernel.  Both against the oracle (rel 1e-5),
+    with odd query / key counts (partial 16-row and 16-key tiles), GQA, right padding, the
+    in-place merge of a second key block, and a one-row (decode-shaped) query."""
+    g = torch.Generator().manual_seed(D)
+    B, Sq, Sk, Hq, Hkv = 2, 45, 333, 8, 2
+    q = torch.randn(B, Sq, Hq, D + 1, generator=g)
+    k = torch.randn(B, Sk, Hkv, D + 1, generator=g)
+    v = torch.randn(B, Sk, Hkv, D + 1, generator=g)
+    kp = torch.arange(Sk).repeat(B, 1)
+    kp[1, -40:] = -1
+    qp = torch.arange(Sk - Sq, Sk).repeat(B, 1)
+    ro, rl = ref.attention_with_lse(q[..., :D], k[..., :D], v[..., :D], qp, kp)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    for name, sl in (("aligned", slice(0, D)), ("offset", slice(1, D + 1))):
+        if name == "aligned":  # contiguous copies: 16-byte aligned rows
+            qa, ka, va = qd[..., sl].contiguous(), kd[..., sl].contiguous(), vd[..., sl].contiguous()
+            r_o, r_l = ro, rl
+        else:
+            qa, ka, va = qd[..., sl], kd[..., sl], vd[..., sl]
+            r_o, r_l = ref.attention_with_lse(q[..., sl], k[..., sl], v[..., sl], qp, kp)
+        out, lse = cea.attention_with_lse(qa, ka, va, qp.to(dev), kp.to(dev))
+        torch.cuda.synchronize()
+        assert_attention_close(out, lse, r_o, r_l, torch.float32, f"f32 D{D} {name}")
+    # running merge of two key blocks == one call
+    qa, ka, va = qd[..., :D].contiguous(), kd[..., :D].contiguous(), vd[..., :D].contiguous()
+    o2 = torch.zeros(B, Sq, Hq, D, device=dev)
+    l2 = torch.full((B, Hq, Sq), float("-inf"), device=dev)
+    for lo, hi in ((0, 150), (150, Sk)):
+        cea.attention_with_lse_into(o2, l2, qa, ka[:, lo:hi], va[:, lo:hi], qp.to(dev), kp[:, lo:hi].to(dev))
+    torch.cuda.synchronize()
+    assert_attention_close(o2, l2, ro, rl, torch.float32, f"f32 D{D} merged blocks")
+    # one query row per sequence
+    o1, l1 = cea.attention_with_lse(qa[:, -1:], ka, va, qp[:, -1:].to(dev), kp.to(dev))
+    torch.cuda.synchronize()
+    assert_attention_close(o1, l1, ro[:, -1:], rl[:, :, -1:], torch.float32, f"f32 D{D} decode row")

@@ -84,15 +84,17 @@ def test_ring_share_bf16_matches_oracle(cea, dev):
 
 @pytest.mark.parametrize("wire", [torch.bfloat16, torch.float16], ids=["bf16-wire", "f16-wire"])
 def test_ring_share_with_wire_compression(cea, dev, wire):
-    """f32 activations, compressed ring traffic (sequence_parallel.py:101-127, comm.py:275-290):
+    """f64 activations, compressed ring traffic (sequence_parallel.py:101-127, comm.py:275-290):
     blocks from other ranks arrive rounded through the wire dtype (float16 saturating at
     65504), the rank's own block stays at full precision.  Some keys and values exceed the
-    float16 range, so the saturation shows in the result."""
+    float16 range, so the saturation shows in the result.  (f64: keys of magnitude 9e4 make
+    scores of a few hundred, whose f32 rounding alone moves the result by ~1e-4 relative
+    between any two summation orders; in f64 the comparison is exact to 1e-10.)"""
     world, rank, S, hq, hkv, d = 4, 2, 256, 4, 2, 64
     g = torch.Generator().manual_seed(5)
-    q = torch.randn(1, S, hq, d, generator=g) * 0.05
-    k = torch.randn(1, S, hkv, d, generator=g)
-    v = torch.randn(1, S, hkv, d, generator=g)
+    q = torch.randn(1, S, hq, d, generator=g, dtype=torch.float64) * 0.05
+    k = torch.randn(1, S, hkv, d, generator=g, dtype=torch.float64)
+    v = torch.randn(1, S, hkv, d, generator=g, dtype=torch.float64)
     k[0, ::17, :, 3] = 9.0e4
     v[0, ::13, :, 5] = -1.0e5
     pos = torch.arange(S).repeat(1, 1)
@@ -111,9 +113,9 @@ def test_ring_share_with_wire_compression(cea, dev, wire):
               for r, (kr, vr, pr) in enumerate(shards)]
     ro, rl = sp_ref.ring_share(qr, qp, blocks, rank, with_lse=True)
     torch.cuda.synchronize()
-    assert_attention_close(out, lse, ro, rl, torch.float32, f"ring share, {wire} wire")
+    assert_attention_close(out, lse, ro, rl, torch.float64, f"ring share, {wire} wire")
     if wire == torch.float16:  # the unsaturated transfer would differ
-        inf_blocks = [(kr, vr, pr) if r == rank else (kr.half().float(), vr.half().float(), pr)
+        inf_blocks = [(kr, vr, pr) if r == rank else (kr.half().double(), vr.half().double(), pr)
                       for r, (kr, vr, pr) in enumerate(shards)]
         bad, _ = sp_ref.ring_share(qr, qp, inf_blocks, rank, with_lse=True)
         assert not torch.allclose(bad, ro, equal_nan=True)
