@@ -1,10 +1,15 @@
-"""ctypes binding of the C ABI declared in ``include/collab_edge_attn.h``.
+"""Loaders of the native libraries built in-tree (``build.py``) under ``_lib/``.
 
-The shared library is built in-tree (``build.py``) and loaded from ``_lib/``.  There is no
-fallback: when the library is missing or a tensor is not on a ROCm device, the calls raise.
-Status codes map onto the exception types the reference raises for the same conditions
-(``ValueError`` for inconsistent shapes / maps, ``NotImplementedError`` for unsupported
-requests, ``RuntimeError`` for launch failures).
+* :func:`ops` - the PyTorch operators ``torch.ops.collab_edge.*`` (csrc/torch_ops.cpp), the
+  thin C++ layer the package's functions dispatch through: it allocates outputs with
+  PyTorch, takes PyTorch's current stream and calls the C ABI.
+* :func:`load_library` - a ctypes binding of the C ABI itself (``include/collab_edge_attn.h``),
+  for callers and tests that bind the C ABI directly.
+
+There is no fallback: when a library is missing or a tensor is not on a ROCm device, the
+calls raise.  Status codes map onto the exception types the reference raises for the same
+conditions (``ValueError`` for inconsistent shapes / maps, ``NotImplementedError`` for
+unsupported requests, ``RuntimeError`` for launch failures).
 """
 
 from __future__ import annotations
@@ -19,6 +24,7 @@ import torch
 
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "_lib" / "libcollab_edge_attn.so"
+OPS_PATH = PKG_DIR / "_lib" / "libcollab_edge_torch.so"
 HEADER_PATH = PKG_DIR.parent / "include" / "collab_edge_attn.h"
 
 MAX_DIMS = 4
@@ -138,6 +144,30 @@ def load_library(path: Optional[Path] = None):
         return lib
 
 
+_ops = None
+
+
+def ops():
+    """``torch.ops.collab_edge`` (loads the operator library once); raises if it has not
+    been built."""
+    global _ops
+    if _ops is not None:
+        return _ops
+    with _lock:
+        if _ops is None:
+            if not OPS_PATH.exists():
+                raise RuntimeError(
+                    f"native operator library {OPS_PATH} is missing: build it with "
+                    "`python __graft_entry__.py build` (or collaborative-edge-system_amd/build.py)"
+                )
+            torch.ops.load_library(str(OPS_PATH))
+            _ops = torch.ops.collab_edge
+    return _ops
+
+
+DTYPES = {code: dt for dt, code in DTYPE_CODES.items()}
+
+
 def last_error() -> str:
     msg = load_library().cea_last_error()
     return msg.decode() if msg else ""
@@ -212,6 +242,8 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 __all__ = [
     "CeaTensor",
     "LIB_PATH",
+    "OPS_PATH",
+    "ops",
     "HEADER_PATH",
     "MAX_PARTS",
     "check",

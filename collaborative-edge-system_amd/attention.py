@@ -2,10 +2,13 @@
 
 Drop-in for ``collab_infer.parallel.attention`` (collab_infer/parallel/attention.py): same
 function names, signatures, masking rule and ``(out, lse)`` convention.  The compute runs in
-hand-written gfx950 kernels reached through the C ABI of ``include/collab_edge_attn.h``:
+hand-written gfx950 kernels, reached through the PyTorch operators ``torch.ops.collab_edge``
+(a thin C++ layer that allocates outputs and calls the C ABI of
+``include/collab_edge_attn.h`` on PyTorch's current stream):
 
 * bf16 / f16 inputs with head size 64 or 128: matrix-core (MFMA) prefill kernel;
-* other head sizes, f32 and f64 inputs: the generic online-softmax kernel;
+* f32 inputs with head size 64 or 128: the f32 matrix-core kernel;
+* other head sizes and f64 inputs: the generic online-softmax kernel;
 * merges: the HBM-bound exact LSE merge kernels.
 
 Masking is defined by explicit token positions (attention.py:7-13)::
@@ -22,7 +25,6 @@ by element, without host synchronisation.
 from __future__ import annotations
 
 import math
-from ctypes import byref
 from typing import List, Optional, Sequence, Tuple, Union
 
 import torch
@@ -122,33 +124,12 @@ def _check_heads(num_q: int, num_kv: int, mapping: Optional[List[int]]) -> None:
         raise ValueError("kv_map must have one entry per query head")
 
 
-def _launch(q, k, v, q_pos, k_pos, causal, scale, mapping, out, lse, accumulate: bool) -> None:
-    """One kernel call of cea_attention_with_lse on the current stream."""
-    lib = nat.load_library()
-    dev = q.device
-    B, Sq, Hq, D = q.shape
-    Sk, Hkv = k.shape[1], k.shape[2]
-    ws_bytes = lib.cea_attention_workspace_bytes(B, Sq, Hq, Sk, Hkv, D, nat.DTYPE_CODES[q.dtype])
-    ws = nat.workspace(ws_bytes, dev)
-    km, kn = nat.kv_map_arg(mapping)
-    args = [nat.tensor_arg(t) for t in (q, k, v, q_pos, k_pos)]
-    o = nat.tensor_arg(out)
-    l = nat.tensor_arg(lse) if lse is not None else None
-    rc = lib.cea_attention_with_lse(
-        *(byref(a) for a in args), int(bool(causal)), float(scale), km, kn,
-        byref(o), byref(l) if l is not None else None, int(accumulate),
-        ws.data_ptr(), ws.numel(), nat.stream_of(dev))
-    nat.check(rc, "attention_with_lse")
-
-
-def _prepare(q, k, v, q_pos, k_pos, kv_map):
-    nat.require_device(q, k, v, q_pos, k_pos)
+def _prepare(q, k, v, kv_map):
     mapping = _kv_map_list(kv_map)
     _check_heads(q.shape[2], k.shape[2], mapping)
-    q, k, v = (_inner_contiguous(t) for t in (q, k, v))
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"q, k and v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
-    return q, k, v, _positions(q_pos), _positions(k_pos), mapping
+    return mapping
 
 
 def attention_with_lse(
@@ -178,19 +159,16 @@ def attention_with_lse(
     if kv_block is not None and kv_block < 1:
         # the reference's range(0, Sk, 0) raises; a negative block size is rejected too
         raise ValueError("kv_block must be positive")
-    q, k, v, q_pos, k_pos, mapping = _prepare(q, k, v, q_pos, k_pos, kv_map)
-    B, Sq, Hq, D = q.shape
-    out = torch.empty(B, Sq, Hq, D, dtype=acc, device=q.device)
-    lse = torch.empty(B, Hq, Sq, dtype=acc, device=q.device)
+    mapping = _prepare(q, k, v, kv_map)
+    ops = nat.ops()
     if kv_block is not None and kv_block < Sk:
-        out.zero_()
-        lse.fill_(float("-inf"))
+        out, lse = _empty_result(q, acc)
         for start in range(0, Sk, kv_block):
             end = min(start + kv_block, Sk)
-            _launch(q, k[:, start:end], v[:, start:end], q_pos, k_pos[:, start:end], causal,
-                    scale, mapping, out, lse, True)
+            ops.attention_into(out, lse, q, k[:, start:end], v[:, start:end], q_pos,
+                               k_pos[:, start:end], bool(causal), scale, mapping, True, None)
         return out, lse
-    _launch(q, k, v, q_pos, k_pos, causal, scale, mapping, out, lse, False)
+    out, lse = ops.attention(q, k, v, q_pos, k_pos, bool(causal), scale, mapping, True)
     return out, lse
 
 
@@ -227,53 +205,24 @@ def attention_with_lse_into(
     if q.shape[1] == 0 or (k.shape[1] == 0 and final is None):
         return
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
-    q, k, v, q_pos, k_pos, mapping = _prepare(q, k, v, q_pos, k_pos, kv_map)
+    mapping = _prepare(q, k, v, kv_map)
     acc = accumulation_dtype(q.dtype)
     if out.dtype != acc or lse.dtype != acc:
         raise ValueError(f"running (out, lse) must be {acc}")
-    if final is None:
-        _launch(q, k, v, q_pos, k_pos, causal, scale, mapping, out, lse, bool(accumulate))
-        return
-    nat.require_device(final)
-    lib = nat.load_library()
-    B, Sq, Hq, D = q.shape
-    Sk, Hkv = k.shape[1], k.shape[2]
-    ws = nat.workspace(lib.cea_attention_workspace_bytes(B, Sq, Hq, Sk, Hkv, D,
-                                                         nat.DTYPE_CODES[q.dtype]), q.device)
-    km, kn = nat.kv_map_arg(mapping)
-    args = [nat.tensor_arg(t) for t in (q, k, v, q_pos, k_pos, out, lse, final)]
-    rc = lib.cea_attention_merge_final(
-        *(byref(a) for a in args[:5]), int(bool(causal)), float(scale), km, kn,
-        *(byref(a) for a in args[5:]), ws.data_ptr(), ws.numel(), nat.stream_of(q.device))
-    nat.check(rc, "attention_merge_final")
+    nat.ops().attention_into(out, lse, q, k, v, q_pos, k_pos, bool(causal), scale, mapping,
+                             bool(accumulate), final)
 
 
 def merge_attention(
     out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor, lse_b: torch.Tensor
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Exactly combine attention over two disjoint key sets (attention.py:242-250)."""
-    nat.require_device(out_a, lse_a, out_b, lse_b)
-    lib = nat.load_library()
-    out_a, out_b = _inner_contiguous(out_a), _inner_contiguous(out_b)
-    out = torch.empty(out_a.shape, dtype=out_a.dtype, device=out_a.device)
-    lse = torch.empty(lse_a.shape, dtype=lse_a.dtype, device=lse_a.device)
-    a = [nat.tensor_arg(t) for t in (out_a, lse_a, out_b, lse_b, out, lse)]
-    rc = lib.cea_merge_attention(*(byref(x) for x in a), nat.stream_of(out.device))
-    nat.check(rc, "merge_attention")
+    out, lse = nat.ops().merge([out_a, out_b], [lse_a, lse_b], True, None)
     return out, lse
 
 
 def _merge_list(outs, lses, out_dtype=None):
-    lib = nat.load_library()
-    outs = [_inner_contiguous(o) for o in outs]
-    dev = outs[0].device
-    out = torch.empty(outs[0].shape, dtype=out_dtype or outs[0].dtype, device=dev)
-    lse = torch.empty(lses[0].shape, dtype=lses[0].dtype, device=dev)
-    oa, la = nat.tensor_array(outs), nat.tensor_array(lses)
-    o, l = nat.tensor_arg(out), nat.tensor_arg(lse)
-    rc = lib.cea_merge_attention_list(len(outs), oa, la, byref(o), byref(l),
-                                      nat.stream_of(dev))
-    nat.check(rc, "merge_attention_list")
+    out, lse = nat.ops().merge(list(outs), list(lses), False, out_dtype)
     return out, lse
 
 
@@ -286,7 +235,6 @@ def merge_attention_list(
         raise ValueError("need the same positive number of outputs and lses")
     if len(outs) == 1:
         return outs[0], lses[0]
-    nat.require_device(*outs, *lses)
     while len(outs) > nat.MAX_PARTS:  # merge is associative: reduce in groups
         grouped = [
             _merge_list(outs[i : i + nat.MAX_PARTS], lses[i : i + nat.MAX_PARTS])
@@ -305,15 +253,10 @@ def pack_partial(out: torch.Tensor, lse: torch.Tensor,
     and, in the last slot, ``lse`` (sequence_parallel.py:275,
     ``torch.cat([o, l.transpose(1, 2).unsqueeze(-1)], dim=-1)``).  ``packed`` may be a slot
     of a preallocated gathered buffer ``[n, B, Sq, H, D+1]``."""
-    nat.require_device(out, lse, packed)
-    B, Sq, H, D = out.shape
     if packed is None:
+        B, Sq, H, D = out.shape
         packed = torch.empty(B, Sq, H, D + 1, dtype=out.dtype, device=out.device)
-    out = _inner_contiguous(out)
-    lib = nat.load_library()
-    a = [nat.tensor_arg(t) for t in (out, lse, packed)]
-    rc = lib.cea_pack_partial(*(byref(x) for x in a), nat.stream_of(out.device))
-    nat.check(rc, "pack_partial")
+    nat.ops().pack_partial(out, lse, packed)
     return packed
 
 
@@ -328,23 +271,12 @@ def merge_packed(gathered, out_dtype: Optional[torch.dtype] = None, return_lse: 
     parts = list(gathered.unbind(0)) if isinstance(gathered, torch.Tensor) else list(gathered)
     if not parts:
         raise ValueError("need at least one packed partial")
-    nat.require_device(*parts)
-    parts = [_inner_contiguous(p) for p in parts]
-    B, Sq, H, D1 = parts[0].shape
-    dev = parts[0].device
     if len(parts) > nat.MAX_PARTS:  # merge is associative: reduce in groups, then repack
         groups = [merge_packed(parts[i : i + nat.MAX_PARTS], return_lse=True)
                   for i in range(0, len(parts), nat.MAX_PARTS)]
         parts = [pack_partial(o, l) for o, l in groups]
-    out = torch.empty(B, Sq, H, D1 - 1, dtype=out_dtype or parts[0].dtype, device=dev)
-    lse = torch.empty(B, H, Sq, dtype=parts[0].dtype, device=dev) if return_lse else None
-    lib = nat.load_library()
-    pa, oa = nat.tensor_array(parts), nat.tensor_arg(out)
-    la = nat.tensor_arg(lse) if lse is not None else None
-    rc = lib.cea_merge_packed(len(parts), pa, byref(oa), byref(la) if la is not None else None,
-                              nat.stream_of(dev))
-    nat.check(rc, "merge_packed")
-    return (out, lse) if return_lse else out
+    res = nat.ops().merge_packed(parts, out_dtype or parts[0].dtype, bool(return_lse))
+    return (res[0], res[1]) if return_lse else res[0]
 
 
 def attention(
@@ -368,10 +300,8 @@ def attention(
     if Sk == 0 or q.shape[1] == 0:
         return torch.zeros_like(q)
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
-    q, k, v, q_pos, k_pos, mapping = _prepare(q, k, v, q_pos, k_pos, kv_map)
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    _launch(q, k, v, q_pos, k_pos, causal, scale, mapping, out, None, False)
-    return out
+    mapping = _prepare(q, k, v, kv_map)
+    return nat.ops().attention(q, k, v, q_pos, k_pos, bool(causal), scale, mapping, False)[0]
 
 
 __all__ = [

@@ -2,7 +2,9 @@
 
 Compiles every ``csrc/*.hip`` translation unit with ``hipcc --offload-arch=gfx950`` (in
 parallel, one process per file) and links them into ``_lib/libcollab_edge_attn.so`` inside
-the package, so the library travels with the source tree.  Run ``python build.py`` or call
+the package, so the library travels with the source tree; then compiles the PyTorch operator
+layer ``csrc/torch_ops.cpp`` (host C++) into ``_lib/libcollab_edge_torch.so``, linked against
+the kernel library.  Run ``python build.py`` or call
 :func:`build`.
 """
 
@@ -20,10 +22,12 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 OBJ_DIR = PKG_DIR / "_lib" / "obj"
 LIB_PATH = PKG_DIR / "_lib" / "libcollab_edge_attn.so"
+OPS_PATH = PKG_DIR / "_lib" / "libcollab_edge_torch.so"
 INCLUDE = REPO_DIR / "include"
 ARCH = os.environ.get("CEA_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+CXX = shutil.which("g++") or "c++"
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -67,23 +71,59 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def _torch_flags():
+    """Include / library directories and ABI flag of the installed PyTorch (host C++ only)."""
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    inc = [f"-I{p}" for p in ce.include_paths()]
+    libdirs = ce.library_paths()
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return inc, libdirs, abi
+
+
+def _compile_ops(inc, abi) -> Path:
+    """The PyTorch operator layer (csrc/torch_ops.cpp): host C++ against torch's headers."""
+    obj = OBJ_DIR / "torch_ops.o"
+    rocm_inc = os.environ.get("ROCM_PATH", "/opt/rocm") + "/include"
+    cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", *inc, f"-I{rocm_inc}", f"-I{INCLUDE}", "-c",
+           str(CSRC / "torch_ops.cpp"), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"torch_ops.cpp failed to compile:\n{proc.stderr}")
+    return obj
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compiles all kernels and links the shared library; returns its path."""
+    """Compiles all kernels and links the kernel library, then the PyTorch operator library
+    on top of it; returns the kernel library's path."""
     OBJ_DIR.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4)), 16)
+    inc, libdirs, abi = _torch_flags()
+    jobs = jobs or min(len(sources) + 1, max(1, (os.cpu_count() or 4)), 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        ops_obj = pool.submit(_compile_ops, inc, abi)
         objs = list(pool.map(_compile, sources))
+        ops_obj = ops_obj.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, LIB_PATH)
+    tmp = OPS_PATH.with_suffix(".so.tmp")
+    cmd = [CXX, "-shared", "-fPIC", "-o", str(tmp), str(ops_obj), f"-L{LIB_PATH.parent}",
+           "-lcollab_edge_attn", *[f"-L{d}" for d in libdirs], "-ltorch", "-ltorch_cpu", "-lc10",
+           "-lc10_hip", "-Wl,-rpath,$ORIGIN", *[f"-Wl,-rpath,{d}" for d in libdirs]]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"operator library link failed:\n{proc.stderr}")
+    os.replace(tmp, OPS_PATH)
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH} and {OPS_PATH}")
     return LIB_PATH
 
 

@@ -12,7 +12,6 @@ Keys and values share one allocation; capacity grows by the reference's rule
 
 from __future__ import annotations
 
-from ctypes import byref
 from typing import Optional, Tuple
 
 import torch
@@ -26,29 +25,11 @@ def kv_append(cache_k: torch.Tensor, cache_v: torch.Tensor, cache_pos: torch.Ten
     """Writes ``k`` (rotated with ``cos``/``sin`` when given) and ``v`` ``[B, n, H, D]`` into
     the head-major caches ``[B, H, cap, D]`` at slots ``offset .. offset+n-1`` and ``pos``
     ``[B, n]`` into ``cache_pos`` ``[B, cap]``, in place."""
-    nat.require_device(cache_k, cache_v, cache_pos, k, v, pos)
     if (cos is None) != (sin is None):
         raise ValueError("give both rotary tables or neither")
-    if k.stride(-1) != 1:
-        k = k.contiguous()
-    if v.stride(-1) != 1:
-        v = v.contiguous()
     if v.dtype != k.dtype or cache_k.dtype != k.dtype or cache_v.dtype != k.dtype:
         raise ValueError("k, v and the caches must share one dtype")
-    pos = pos.to(torch.int64)
-    if cos is not None:
-        nat.require_device(cos, sin)
-        cos, sin = cos.to(k.dtype), sin.to(k.dtype)
-        cos = cos if cos.stride(-1) == 1 else cos.contiguous()
-        sin = sin if sin.stride(-1) == 1 else sin.contiguous()
-    a = [nat.tensor_arg(t) for t in (k, v, pos)]
-    tabs = [nat.tensor_arg(cos), nat.tensor_arg(sin)] if cos is not None else None
-    dst = [nat.tensor_arg(t) for t in (cache_k, cache_v, cache_pos)]
-    rc = nat.load_library().cea_kv_append(
-        byref(a[0]), byref(a[1]), byref(a[2]),
-        byref(tabs[0]) if tabs else None, byref(tabs[1]) if tabs else None,
-        byref(dst[0]), byref(dst[1]), byref(dst[2]), int(offset), nat.stream_of(k.device))
-    nat.check(rc, "kv_append")
+    nat.ops().kv_append(cache_k, cache_v, cache_pos, int(offset), k, v, pos, cos, sin)
 
 
 class LayerKVCache:

@@ -17,7 +17,6 @@ transcendental functions).
 from __future__ import annotations
 
 import math
-from ctypes import byref
 from typing import Optional
 
 import torch
@@ -65,16 +64,7 @@ def _rows(x: torch.Tensor) -> torch.Tensor:
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """Functional RMSNorm with the reference's rounding (llama.py:58-61)."""
-    nat.require_device(x, weight)
-    out_dtype = torch.promote_types(weight.dtype, x.dtype)
-    x2 = _rows(x)
-    y = torch.empty(x2.shape, dtype=out_dtype, device=x.device)
-    w = weight if weight.stride(-1) == 1 else weight.contiguous()
-    a = [nat.tensor_arg(t) for t in (x2, w, y)]
-    rc = nat.load_library().cea_rmsnorm(byref(a[0]), byref(a[1]), float(eps), byref(a[2]),
-                                        nat.stream_of(x.device))
-    nat.check(rc, "rmsnorm")
-    return y.view(x.shape)
+    return nat.ops().rmsnorm(_rows(x), weight, float(eps)).view(x.shape)
 
 
 class RMSNorm(nn.Module):
@@ -91,19 +81,9 @@ class RMSNorm(nn.Module):
 
 def rope_tables(positions: torch.Tensor, inv_freq: torch.Tensor, dtype: torch.dtype):
     """``(cos, sin)`` tables ``[B, S, D]`` in ``dtype`` at explicit positions (llama.py:74-77)."""
-    nat.require_device(positions, inv_freq)
-    pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
-    if pos.dim() == 1:
-        pos = pos.unsqueeze(0)
+    pos = positions.unsqueeze(0) if positions.dim() == 1 else positions
     want = torch.float64 if dtype == torch.float64 else torch.float32
-    inv = inv_freq.to(want).contiguous()
-    B, S = pos.shape
-    D = 2 * inv.shape[0]
-    cos = torch.empty(B, S, D, dtype=dtype, device=pos.device)
-    sin = torch.empty(B, S, D, dtype=dtype, device=pos.device)
-    a = [nat.tensor_arg(t) for t in (pos, inv, cos, sin)]
-    rc = nat.load_library().cea_rope_tables(*(byref(x) for x in a), nat.stream_of(pos.device))
-    nat.check(rc, "rope_tables")
+    cos, sin = nat.ops().rope_tables(pos, inv_freq.to(want).contiguous(), dtype)
     return cos, sin
 
 
@@ -131,41 +111,24 @@ class RotaryEmbedding(nn.Module):
 
 def apply_rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """``x``: ``[B, S, H, D]``; ``cos``/``sin``: ``[B, S, D]`` (llama.py:85-88)."""
-    nat.require_device(x, cos, sin)
-    if x.stride(-1) != 1:
-        x = x.contiguous()
     if cos.dtype != x.dtype or sin.dtype != x.dtype:
         # the reference multiplies in the promoted dtype; tables in the model dtype are the
         # convention of RotaryEmbedding, other combinations are converted explicitly
         cos, sin = cos.to(x.dtype), sin.to(x.dtype)
-    cos = cos if cos.stride(-1) == 1 else cos.contiguous()
-    sin = sin if sin.stride(-1) == 1 else sin.contiguous()
-    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    a = [nat.tensor_arg(t) for t in (x, cos, sin, out)]
-    rc = nat.load_library().cea_apply_rotary(*(byref(t) for t in a), nat.stream_of(x.device))
-    nat.check(rc, "apply_rotary")
-    return out
+    return nat.ops().apply_rotary(x, cos, sin)
 
 
 def rmsnorm_rope(x: torch.Tensor, weight: torch.Tensor, eps: float, positions: torch.Tensor,
                  inv_freq: torch.Tensor, num_heads: int) -> torch.Tensor:
     """RMSNorm of ``x`` ``[S, H*D]`` followed by rotary at ``positions`` ``[S]`` on the
     ``[1, S, H, D]`` view, in one kernel.  Returns ``[1, S, H, D]``."""
-    nat.require_device(x, weight, positions, inv_freq)
     x2 = _rows(x)
     S, C = x2.shape
     if C % num_heads:
         raise ValueError(f"{C} features do not split into {num_heads} heads")
-    pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
-    pos = pos.reshape(-1)
     want = torch.float64 if x.dtype == torch.float64 else torch.float32
-    inv = inv_freq.to(want).contiguous()
-    out = torch.empty(S, C, dtype=x.dtype, device=x.device)
-    a = [nat.tensor_arg(t) for t in (x2, weight, pos, inv, out)]
-    rc = nat.load_library().cea_rmsnorm_rope(byref(a[0]), byref(a[1]), float(eps), byref(a[2]),
-                                             byref(a[3]), int(num_heads), byref(a[4]),
-                                             nat.stream_of(x.device))
-    nat.check(rc, "rmsnorm_rope")
+    out = nat.ops().rmsnorm_rope(x2, weight, float(eps), positions.reshape(-1),
+                                 inv_freq.to(want).contiguous(), int(num_heads))
     return out.view(1, S, num_heads, C // num_heads)
 
 
@@ -178,16 +141,9 @@ def gated_mul(gate: torch.Tensor, up: torch.Tensor, act: str = "silu") -> torch.
     activations; ``gate``/``up`` may be column halves of one fused GEMM output."""
     if act not in ACTIVATION_CODES:
         raise NotImplementedError(f"activation {act!r} is not supported")
-    nat.require_device(gate, up)
     if gate.shape != up.shape:
         raise ValueError(f"gate {tuple(gate.shape)} and up {tuple(up.shape)} differ")
-    g2, u2 = _rows(gate), _rows(up)
-    out = torch.empty(g2.shape, dtype=gate.dtype, device=gate.device)
-    a = [nat.tensor_arg(t) for t in (g2, u2, out)]
-    rc = nat.load_library().cea_gated_mul(*(byref(t) for t in a), ACTIVATION_CODES[act],
-                                          nat.stream_of(gate.device))
-    nat.check(rc, "gated_mul")
-    return out.view(gate.shape)
+    return nat.ops().gated_mul(_rows(gate), _rows(up), ACTIVATION_CODES[act]).view(gate.shape)
 
 
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:

@@ -22,7 +22,6 @@ A group of size 1 is the single-device case of the reference (its ``n == 1`` bra
 
 from __future__ import annotations
 
-from ctypes import byref
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -240,45 +239,19 @@ def partitioned_attention(
     if len(parts) > nat.MAX_PARTS:
         raise NotImplementedError(f"at most {nat.MAX_PARTS} partitions per call")
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
-    nat.require_device(q, q_pos, *[t for p in parts for t in p])
     mapping = _kv_map_list(kv_map)
-    q = _inner_contiguous(q)
-    q_pos = _positions(q_pos)
-    ks = [_inner_contiguous(p[0]) for p in parts]
-    vs = [_inner_contiguous(p[1]) for p in parts]
-    ps = [_positions(p[2]) for p in parts]
-    for kk in ks:
-        _check_heads(q.shape[2], kk.shape[2], mapping)
-    B, Sq, Hq, D = q.shape
+    for p in parts:
+        _check_heads(q.shape[2], p[0].shape[2], mapping)
     acc = accumulation_dtype(q.dtype)
     if out_dtype is None:  # the merged lse comes with an accumulation-precision output
         out_dtype = acc if return_lse else q.dtype
-    out = torch.empty(B, Sq, Hq, D, dtype=out_dtype, device=q.device)
-    lse = torch.empty(B, Hq, Sq, dtype=acc, device=q.device) if return_lse else None
-    lib = nat.load_library()
-    n = len(parts)
-    part_out = part_lse = None
-    if return_parts:
-        part_out = [torch.empty(B, Sq, Hq, D, dtype=acc, device=q.device) for _ in range(n)]
-        part_lse = [torch.empty(B, Hq, Sq, dtype=acc, device=q.device) for _ in range(n)]
-    import ctypes
-
-    sks = (ctypes.c_int64 * n)(*[kk.shape[1] for kk in ks])
-    ws_bytes = lib.cea_partitioned_attention_workspace_bytes(
-        n, sks, B, Sq, Hq, ks[0].shape[2], D, nat.DTYPE_CODES[q.dtype])
-    ws = nat.workspace(ws_bytes, q.device)
-    km, kn = nat.kv_map_arg(mapping)
-    qa, qpa = nat.tensor_arg(q), nat.tensor_arg(q_pos)
-    ka, va, pa = nat.tensor_array(ks), nat.tensor_array(vs), nat.tensor_array(ps)
-    oa = nat.tensor_arg(out)
-    la = nat.tensor_arg(lse) if lse is not None else None
-    poa = nat.tensor_array(part_out) if part_out else None
-    pla = nat.tensor_array(part_lse) if part_lse else None
-    rc = lib.cea_partitioned_attention(
-        byref(qa), n, ka, va, byref(qpa), pa, int(bool(causal)), float(scale), km, kn, poa, pla,
-        byref(oa), byref(la) if la is not None else None, ws.data_ptr(), ws.numel(),
-        nat.stream_of(q.device))
-    nat.check(rc, "partitioned_attention")
+    res = nat.ops().partitioned(q, q_pos, [p[0] for p in parts], [p[1] for p in parts],
+                                [p[2] for p in parts], bool(causal), scale, mapping, out_dtype,
+                                bool(return_lse), bool(return_parts))
+    out = res[0]
+    lse = res[1] if return_lse else None
+    rest = res[2 if return_lse else 1:]
+    part_out, part_lse = rest[0::2], rest[1::2]
     result = [out]
     if return_lse:
         result.append(lse)
@@ -398,18 +371,9 @@ def ulysses_scatter(q, k, v, positions, comm: LocalGroup, seq_sizes: Sequence[in
             sq, sk, sv = (comm.received(x) for x in (sq, sk, sv))
         shards.append((_heads_contiguous(sq), _heads_contiguous(sk), _heads_contiguous(sv),
                        _positions(sp)))
-    nat.require_device(*[t for sh in shards for t in sh])
-    B, _, _, D = q.shape
-    S = sum(sh[0].shape[1] for sh in shards)
-    width = me.q_count + 2 * me.kv_count
-    full = torch.empty(B, S, width, D, dtype=q.dtype, device=q.device)
-    pos_f = torch.empty(B, S, dtype=torch.int64, device=q.device)
-    lib = nat.load_library()
-    qa, ka, va, pa = (nat.tensor_array([sh[i] for sh in shards]) for i in range(4))
-    fa, pfa = nat.tensor_arg(full), nat.tensor_arg(pos_f)
-    rc = lib.cea_ulysses_scatter(n, qa, ka, va, pa, me.q_start, me.q_count, me.kv_start,
-                                 me.kv_count, byref(fa), byref(pfa), nat.stream_of(q.device))
-    nat.check(rc, "ulysses_scatter")
+    full, pos_f = nat.ops().ulysses_scatter([sh[0] for sh in shards], [sh[1] for sh in shards],
+                                            [sh[2] for sh in shards], [sh[3] for sh in shards],
+                                            me.q_start, me.q_count, me.kv_start, me.kv_count)
     q_f, k_f, v_f = full.split([me.q_count, me.kv_count, me.kv_count], dim=2)
     return q_f, k_f, v_f, pos_f
 
@@ -417,16 +381,7 @@ def ulysses_scatter(q, k, v, positions, comm: LocalGroup, seq_sizes: Sequence[in
 def _head_concat(outs: Sequence[torch.Tensor], start: int, length: int) -> torch.Tensor:
     """Tokens ``[start, start + length)`` of every part ``[B, S, h_j, D]``, heads
     concatenated in part order, by one kernel (``cea_ulysses_gather``)."""
-    outs = [_heads_contiguous(o) for o in outs]
-    nat.require_device(*outs)
-    B, _, _, D = outs[0].shape
-    H = sum(o.shape[2] for o in outs)
-    res = torch.empty(B, length, H, D, dtype=outs[0].dtype, device=outs[0].device)
-    lib = nat.load_library()
-    oa, ra = nat.tensor_array(outs), nat.tensor_arg(res)
-    rc = lib.cea_ulysses_gather(len(outs), oa, int(start), byref(ra), nat.stream_of(res.device))
-    nat.check(rc, "ulysses_gather")
-    return res
+    return nat.ops().ulysses_gather([_heads_contiguous(o) for o in outs], int(start), int(length))
 
 
 def ulysses_gather(out_heads: torch.Tensor, comm: LocalGroup, seq_sizes: Sequence[int],

@@ -130,3 +130,38 @@ def test_python_api_validates_heads_before_device_work(cea):
     assert cea.gqa_group(8, 2, [0, 1, 0, 1, 0, 1, 0, 1]) is None
     with pytest.raises(ValueError, match="one entry per query head"):
         cea.expand_kv(k, 4, kv_map=[0, 1])
+
+
+OPS = ["attention", "attention_into", "merge", "partitioned", "pack_partial", "merge_packed",
+       "ulysses_scatter", "ulysses_gather", "rmsnorm", "rope_tables", "apply_rotary",
+       "rmsnorm_rope", "gated_mul", "kv_append"]
+
+
+def test_torch_operator_library_registers_every_op(cea):
+    """The PyTorch operator layer (csrc/torch_ops.cpp) loads on top of the C ABI library and
+    registers the operators the package dispatches through."""
+    assert cea._native.OPS_PATH.exists(), "build the libraries first (__graft_entry__.build())"
+    ops = cea._native.ops()
+    for name in OPS:
+        assert hasattr(ops, name), f"torch.ops.collab_edge.{name} missing"
+    # the package's functions go through these operators, not through ctypes
+    import inspect
+
+    for mod in (cea.attention, cea.layers, cea.sequence_parallel, cea.kv_cache):
+        src = inspect.getsource(mod)
+        assert "nat.ops()" in src and "byref" not in src, mod.__name__
+
+
+def test_operators_refuse_host_tensors(cea):
+    """No host path: CPU tensors raise RuntimeError before any work."""
+    ops = cea._native.ops()
+    q = torch.zeros(1, 4, 2, 8)
+    pos = torch.arange(4).view(1, 4)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.attention(q, q, q, pos, pos, True, 0.35, None, True)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.gated_mul(q.view(4, 16), q.view(4, 16), 0)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        cea.attention_with_lse(q, q, q, pos, pos)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        cea.rmsnorm(q, torch.ones(8), 1e-5)
