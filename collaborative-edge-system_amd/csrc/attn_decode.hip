@@ -489,11 +489,14 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
     float2 a = {0.f, 0.f};
 #pragma unroll 8
     for (int j = c0 + wave; j < c1; j += RWAVES) {
-      // chunks without a visible key have weight 0 and unwritten outputs: select, not multiply
-      const float w = w_s[j];
-      const float2 o = *(const float2*)(base + j * cstride + 2 * lane);
-      a.x = w != 0.f ? __builtin_fmaf(o.x, w, a.x) : a.x;
-      a.y = w != 0.f ? __builtin_fmaf(o.y, w, a.y) : a.y;
+      // chunks without a visible key have weight 0 and unwritten outputs: they are not read
+      // (the weight is the same for the whole wave, so the load is skipped, not masked)
+      const float w = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(w_s[j])));
+      if (w != 0.f) {
+        const float2 o = *(const float2*)(base + j * cstride + 2 * lane);
+        a.x = __builtin_fmaf(o.x, w, a.x);
+        a.y = __builtin_fmaf(o.y, w, a.y);
+      }
     }
     acc_s[wave][lane] = a;
     __syncthreads();

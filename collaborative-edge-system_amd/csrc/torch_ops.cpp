@@ -13,7 +13,10 @@
 #include <torch/library.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "collab_edge_attn.h"
@@ -84,8 +87,21 @@ void* stream_of(const at::Device& d) {
   return (void*)c10::hip::getCurrentHIPStream(d.index()).stream();
 }
 
+// The kernels' workspace: one buffer per (device, stream), grown to the largest request seen
+// and then reused by every call on that stream (calls on one stream run in order, so a call
+// never overwrites scratch a queued call still reads).  A grown-out buffer returns to
+// PyTorch's caching allocator, which hands its memory out again only in stream order.
+std::mutex g_ws_mu;
+std::map<std::pair<int, void*>, Tensor> g_ws;
+
 Tensor workspace(size_t bytes, const at::Device& d) {
-  return at::empty({(int64_t)std::max<size_t>(bytes, 256)}, at::TensorOptions().dtype(at::kByte).device(d));
+  void* st = stream_of(d);
+  const int64_t want = (int64_t)std::max<size_t>((bytes + 4095) & ~(size_t)4095, 4096);
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  Tensor& t = g_ws[{(int)d.index(), st}];
+  if (!t.defined() || t.numel() < want)
+    t = at::empty({want}, at::TensorOptions().dtype(at::kByte).device(d));
+  return t;
 }
 
 // q / k / v style operands need a unit innermost stride
