@@ -183,8 +183,14 @@ def bench_layers(cea, torch, steps, warmup, dev):
     gbs = w.silu_bytes / sec / 1e9
     res["silu_mul"] = {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                        "us_per_step": round(sec * 1e6, 2), "bytes": w.silu_bytes}
-    res["workload"] = ("bf16 RMSNorm+rotary [4096,4096]->32x128 theta 1e4; SiLU-gate [4096,14336]; "
-                       "timed as HIP-graph replays of 20 launches")
+    for act in ("gelu", "gelu_pytorch_tanh"):  # the reference's other gated activations
+        sec = _graph_timed(lambda: cea.gated_mul(g, u, act), steps, warmup, torch)
+        gbs = w.silu_bytes / sec / 1e9
+        res[f"{act}_mul"] = {"value": round(gbs, 1), "unit": "GB/s",
+                             "frac": round(gbs / PEAK_HBM_GBS, 4),
+                             "us_per_step": round(sec * 1e6, 2), "bytes": w.silu_bytes}
+    res["workload"] = ("bf16 RMSNorm+rotary [4096,4096]->32x128 theta 1e4; SiLU-gate (and the GELU "
+                       "gates) [4096,14336]; timed as HIP-graph replays of 20 launches")
     return res
 
 

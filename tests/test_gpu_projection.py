@@ -1,9 +1,6 @@
-"""The fused projection module (tensor_parallel.py:264-320) on the device against the
-oracle's ``F.linear`` on the CPU, and its column views fed to the kernels without copies.
-
-Tolerance: the GEMM accumulates in f32 in another order than the CPU, so each output may sit
-on the other side of one rounding step of the output dtype: |gpu - cpu| <= 1 ulp of the
-output dtype at |cpu| plus 1e-4 of max |cpu|, for every element (f32: 1e-5 normwise).
+"""The column views of the fused Q/K/V projection output (tensor_parallel.py:294-295) feed the
+attention kernels without copies: attention on the strided views equals attention on
+contiguous copies, bit for bit.  (The GEMM itself is PyTorch's and is not tested here.)
 """
 
 import pytest
@@ -28,23 +25,6 @@ def _check(got: torch.Tensor, want: torch.Tensor):
         return
     err = (got - want).abs()
     assert bool((err <= _ulp(want, dtype) + 1e-4 * want.abs().max()).all()), err.max().item()
-
-
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=str)
-@pytest.mark.parametrize("N,K,M,bias", [(1, 64, 96, False), (37, 256, 384, True), (300, 1024, 640, False),
-                                        (513, 512, 1536, True), (64, 4096, 1, True)])
-def test_linear_matches_oracle(cea, dev, dtype, N, K, M, bias):
-    g = torch.Generator().manual_seed(N + K + M)
-    x = torch.randn(N, K, generator=g).to(dtype)
-    w = (torch.randn(M, K, generator=g) / K ** 0.5).to(dtype)
-    b = torch.randn(M, generator=g).to(dtype) if bias else None
-    got = cea.linear(x.to(dev), w.to(dev), b.to(dev) if bias else None)
-    want = L.linear(x.float(), w.float(), b.float() if bias else None).to(dtype)
-    torch.cuda.synchronize()
-    assert got.dtype == dtype and got.shape == (N, M)
-    if dtype == torch.float32:
-        want = L.linear(x.double(), w.double(), b.double() if bias else None)
-    _check(got, want)
 
 
 def test_fused_qkv_projection_views_feed_the_kernels(cea, dev):
