@@ -37,14 +37,14 @@ def _log(msg: str) -> None:
 
 
 def _measured_traffic(name: str):
-    """HBM bytes per launch of a kernel, from the FETCH_SIZE / WRITE_SIZE counter runs
-    summarised in profiles/<name>_pmc.md (line ``traffic_bytes_per_launch: N``), or None."""
+    """HBM bytes per launch of a kernel, from the TCC request-counter runs summarised in
+    profiles/<name>_pmc.md (line ``traffic_bytes_per_launch: N ...``), or None."""
     path = ROOT / "profiles" / f"{name}_pmc.md"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":", 1)[1].strip())
+            return int(line.split(":", 1)[1].split()[0])
     return None
 
 
