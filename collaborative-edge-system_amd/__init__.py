@@ -10,7 +10,8 @@ Import with ``importlib.import_module("collaborative-edge-system_amd")``.  Modul
 * :mod:`.kv_cache` - head-major KV cache with the rotary of K fused into the append
   (collab_infer/models/cache.py)
 * :mod:`.partition` - splits and sequence layouts (collab_infer/parallel/partition.py)
-* :mod:`.projection` - the fused Q/K/V and gate/up projections (torch's GEMM, column views)
+* :mod:`.projection` - the fused Q/K/V and gate/up projections (own gfx950 GEMM; column views,
+  gate/up with the activation fused)
   (collab_infer/parallel/tensor_parallel.py:264-320)
 * :mod:`.workloads` - seeded inputs of the five measured workloads
 * :mod:`.parallel` / :mod:`.models` - the reference's import paths
@@ -47,7 +48,7 @@ from .layers import (  # noqa: F401
     silu_mul,
 )
 from .partition import HeadShard, SequenceLayout, partition_heads, split_sizes  # noqa: F401
-from .projection import FusedColumnParallelLinear, fused_linear, linear  # noqa: F401
+from .projection import FusedColumnParallelLinear, fused_linear, linear, linear_gated  # noqa: F401
 from .sequence_parallel import (  # noqa: F401
     LocalGroup,
     distributed_kv_attention,

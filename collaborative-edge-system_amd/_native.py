@@ -103,6 +103,8 @@ _SIGNATURES = {
     ),
     "cea_silu_mul": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p]),
     "cea_gated_mul": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.c_void_p]),
+    "cea_linear": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_void_p]),
+    "cea_linear_gated": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_void_p]),
     "cea_kv_append": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int64, ctypes.c_void_p],

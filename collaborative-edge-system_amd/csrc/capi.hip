@@ -913,4 +913,70 @@ int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, 
   return cea_gated_mul(gate, up, out, CEA_ACT_SILU, stream);
 }
 
+// x [M, K]; weight rows [N, K] (innermost stride 1, any row stride); bias [N] or NULL
+static int check_projection(const char* what, const cea_tensor* x, const cea_tensor* w,
+                            const cea_tensor* b, const char* wname, const char* bname) {
+  int rc;
+  if ((rc = check_tensor(w, wname, 2, x->dtype, true))) return rc;
+  CEA_REQUIRE(w->size[1] == x->size[1], CEA_EINVAL,
+              "%s: %s has %lld input features, x has %lld", what, wname, (long long)w->size[1],
+              (long long)x->size[1]);
+  CEA_REQUIRE(w->size[0] <= 1 || w->stride[0] >= w->size[1], CEA_EINVAL,
+              "%s: %s rows overlap", what, wname);
+  if (b != nullptr) {
+    if ((rc = check_tensor(b, bname, 1, x->dtype, true))) return rc;
+    CEA_REQUIRE(b->size[0] == w->size[0], CEA_EINVAL, "%s: %s must be [%lld]", what, bname,
+                (long long)w->size[0]);
+  }
+  return CEA_OK;
+}
+
+static int check_linear_io(const char* what, const cea_tensor* x, const cea_tensor* y,
+                           int64_t n) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 2, -1, true))) return rc;
+  CEA_REQUIRE(x->dtype == CEA_BF16 || x->dtype == CEA_F16 || x->dtype == CEA_F32 ||
+                  x->dtype == CEA_F64,
+              CEA_EUNSUPPORTED, "%s: unsupported dtype %s", what, dtype_name(x->dtype));
+  CEA_REQUIRE(x->size[0] <= 1 || x->stride[0] >= x->size[1], CEA_EINVAL, "%s: x rows overlap",
+              what);
+  if ((rc = check_tensor(y, "y", 2, x->dtype, true))) return rc;
+  CEA_REQUIRE(y->size[0] == x->size[0] && y->size[1] == n, CEA_EINVAL,
+              "%s: y must be [%lld, %lld]", what, (long long)x->size[0], (long long)n);
+  CEA_REQUIRE(y->size[0] <= 1 || y->stride[0] >= y->size[1], CEA_EINVAL, "%s: y rows overlap",
+              what);
+  return CEA_OK;
+}
+
+int cea_linear(const cea_tensor* x, const cea_tensor* weight, const cea_tensor* bias,
+               cea_tensor* y, void* stream) {
+  int rc;
+  CEA_REQUIRE(x != nullptr && weight != nullptr, CEA_EINVAL, "linear: missing tensor");
+  if ((rc = check_tensor(weight, "weight", 2, -1, true))) return rc;
+  if ((rc = check_linear_io("linear", x, y, weight->size[0]))) return rc;
+  if ((rc = check_projection("linear", x, weight, bias, "weight", "bias"))) return rc;
+  return launch_linear(x, weight, nullptr, bias, nullptr, y, 0, 0, (hipStream_t)stream);
+}
+
+int cea_linear_gated(const cea_tensor* x, const cea_tensor* w_gate, const cea_tensor* w_up,
+                     const cea_tensor* b_gate, const cea_tensor* b_up, cea_tensor* y,
+                     int32_t act, void* stream) {
+  int rc;
+  CEA_REQUIRE(x != nullptr && w_gate != nullptr && w_up != nullptr, CEA_EINVAL,
+              "linear_gated: missing tensor");
+  if ((rc = check_tensor(w_gate, "w_gate", 2, -1, true))) return rc;
+  if ((rc = check_linear_io("linear_gated", x, y, w_gate->size[0]))) return rc;
+  if ((rc = check_projection("linear_gated", x, w_gate, b_gate, "w_gate", "b_gate"))) return rc;
+  if ((rc = check_projection("linear_gated", x, w_up, b_up, "w_up", "b_up"))) return rc;
+  CEA_REQUIRE(w_up->size[0] == w_gate->size[0], CEA_EINVAL,
+              "linear_gated: w_gate and w_up must have the same number of rows");
+  CEA_REQUIRE(w_gate->size[0] <= 1 || w_up->stride[0] == w_gate->stride[0], CEA_EINVAL,
+              "linear_gated: w_gate and w_up must share a row stride");
+  CEA_REQUIRE((b_gate == nullptr) == (b_up == nullptr), CEA_EINVAL,
+              "linear_gated: give both biases or neither");
+  CEA_REQUIRE(act >= CEA_ACT_SILU && act <= CEA_ACT_RELU, CEA_EUNSUPPORTED,
+              "linear_gated: unknown activation %d", (int)act);
+  return launch_linear(x, w_gate, w_up, b_gate, b_up, y, 1, act, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -142,6 +142,37 @@ __device__ __forceinline__ bool is_finite(double x) { return __builtin_isfinite(
 __device__ __forceinline__ bool is_inf(float x) { return __builtin_isinf(x); }
 __device__ __forceinline__ bool is_inf(double x) { return __builtin_isinf(x); }
 
+// Activations of the gated MLP (the reference's _ACTIVATIONS, llama.py:44-49), in f32 for
+// bf16 / f16 / f32 tensors and in f64 for f64, the way torch's elementwise kernels compute
+// them:
+//   silu              g / (1 + exp(-g))
+//   gelu              (g * 0.5) * (1 + erf(g * (1/sqrt 2)))
+//   gelu_pytorch_tanh (0.5 * g) * (1 + tanh(sqrt(2/pi) * (g + 0.044715 * g^3)))
+//   relu              g when g > 0 or g is NaN, else 0
+template <typename M> __device__ __forceinline__ M erf_acc(M x);
+template <> __device__ __forceinline__ float erf_acc<float>(float x) { return erff(x); }
+template <> __device__ __forceinline__ double erf_acc<double>(double x) { return erf(x); }
+template <typename M> __device__ __forceinline__ M tanh_acc(M x);
+template <> __device__ __forceinline__ float tanh_acc<float>(float x) { return tanhf(x); }
+template <> __device__ __forceinline__ double tanh_acc<double>(double x) { return tanh(x); }
+
+template <int ACT, typename M> __device__ __forceinline__ M gate_act(M a) {
+  if constexpr (ACT == CEA_ACT_SILU) {
+    return div_rn(a, add_rn((M)1, exp_acc(-a)));
+  } else if constexpr (ACT == CEA_ACT_GELU) {
+    const M alpha = (M)0.70710678118654752440;  // 1/sqrt(2)
+    return mul_rn(mul_rn(a, (M)0.5), add_rn((M)1, erf_acc<M>(mul_rn(a, alpha))));
+  } else if constexpr (ACT == CEA_ACT_GELU_TANH) {
+    const M beta = (M)0.79788456080286535588;   // sqrt(2/pi)
+    const M kappa = (M)0.044715;
+    const M cube = mul_rn(mul_rn(a, a), a);
+    const M inner = mul_rn(beta, add_rn(a, mul_rn(kappa, cube)));
+    return mul_rn(mul_rn((M)0.5, a), add_rn((M)1, tanh_acc<M>(inner)));
+  } else {
+    return a <= (M)0 ? (M)0 : a;
+  }
+}
+
 // torch.logaddexp semantics: equal infinities return that infinity, otherwise
 // max + log1p(exp(-|a-b|)).
 template <typename A> __device__ __forceinline__ A logaddexp(A a, A b) {

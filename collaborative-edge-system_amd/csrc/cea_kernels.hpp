@@ -154,6 +154,11 @@ int launch_rmsnorm_rope(const cea_tensor* x, const cea_tensor* w, double eps,
                         hipStream_t s);
 int launch_gated_mul(const cea_tensor* g, const cea_tensor* u, cea_tensor* o, int act,
                      hipStream_t s);
+// x [M, K], w_gate / w_up [N, K] (one row stride), biases [N] or null, y [M, N]; mode 0 is
+// the plain projection (w_up / b_up unused), 1 the gated one with activation act
+int launch_linear(const cea_tensor* x, const cea_tensor* wg, const cea_tensor* wu,
+                  const cea_tensor* bg, const cea_tensor* bu, cea_tensor* y, int mode, int act,
+                  hipStream_t s);
 int launch_attn_generic(const AttnParams& p, hipStream_t s);
 int launch_tile_info(const int64_t* k_pos, int64_t kps_b, int64_t kps_s, int32_t B, int32_t Sk,
                      TileInfo* tiles, int32_t ntiles, hipStream_t s);

@@ -57,6 +57,15 @@ __device__ __forceinline__ void buffer_load_lds4_m0(i32x4 rs, uint32_t lds, uint
                ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(rs) : "memory", "m0");
 }
 
+// 16-byte load with a wave-uniform byte offset (soffset) added to the per-lane offset.
+__device__ __forceinline__ void buffer_load_lds16_m0_so(i32x4 rs, uint32_t lds, uint32_t voffset,
+                                                        uint32_t soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(rs),
+                 "s"(__builtin_amdgcn_readfirstlane(soffset))
+               : "memory", "m0");
+}
+
 // Waits until at most N of this wave's vector-memory loads are outstanding.
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");

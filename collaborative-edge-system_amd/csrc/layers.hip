@@ -546,37 +546,8 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
 
 // ---------------------------------------------------------------------------------------
 // Gated activations: out = act(gate) * up, act(gate) rounded to T first (the reference's
-// self.act(gate) * up, llama.py:44-49, 305: two separately rounded tensor ops; the
-// activation itself runs in f32 for bf16 / f16 / f32 and in f64 for f64, as torch's
-// elementwise kernels compute it):
-//   silu              g / (1 + exp(-g))
-//   gelu              (g * 0.5) * (1 + erf(g * (1/sqrt 2)))
-//   gelu_pytorch_tanh (0.5 * g) * (1 + tanh(sqrt(2/pi) * (g + 0.044715 * g^3)))
-//   relu              g when g > 0 or g is NaN, else 0
-template <typename M> __device__ __forceinline__ M erf_acc(M x);
-template <> __device__ __forceinline__ float erf_acc<float>(float x) { return erff(x); }
-template <> __device__ __forceinline__ double erf_acc<double>(double x) { return erf(x); }
-template <typename M> __device__ __forceinline__ M tanh_acc(M x);
-template <> __device__ __forceinline__ float tanh_acc<float>(float x) { return tanhf(x); }
-template <> __device__ __forceinline__ double tanh_acc<double>(double x) { return tanh(x); }
-
-template <int ACT, typename M> __device__ __forceinline__ M gate_act(M a) {
-  if constexpr (ACT == CEA_ACT_SILU) {
-    return div_rn(a, add_rn((M)1, exp_acc(-a)));
-  } else if constexpr (ACT == CEA_ACT_GELU) {
-    const M alpha = (M)0.70710678118654752440;  // 1/sqrt(2)
-    return mul_rn(mul_rn(a, (M)0.5), add_rn((M)1, erf_acc<M>(mul_rn(a, alpha))));
-  } else if constexpr (ACT == CEA_ACT_GELU_TANH) {
-    const M beta = (M)0.79788456080286535588;   // sqrt(2/pi)
-    const M kappa = (M)0.044715;
-    const M cube = mul_rn(mul_rn(a, a), a);
-    const M inner = mul_rn(beta, add_rn(a, mul_rn(kappa, cube)));
-    return mul_rn(mul_rn((M)0.5, a), add_rn((M)1, tanh_acc<M>(inner)));
-  } else {
-    return a <= (M)0 ? (M)0 : a;
-  }
-}
-
+// self.act(gate) * up, llama.py:44-49, 305: two separately rounded tensor ops; gate_act in
+// cea_common.hpp computes the activation as torch's elementwise kernels do)
 template <typename T, int VEC, int ACT>
 __global__ __launch_bounds__(256) void gated_mul_kernel(const T* __restrict__ g, int64_t gs,
                                                         const T* __restrict__ u, int64_t us,

@@ -380,6 +380,77 @@ Tensor gated_mul(const Tensor& gate, const Tensor& up, int64_t act) {
   return out;
 }
 
+// x [..., K] as a 2-D [M, K] view (a copy only when the leading dimensions do not collapse)
+Tensor rows_of(const Tensor& x) {
+  TORCH_CHECK_VALUE(x.dim() >= 1, "x must have at least one dimension");
+  int64_t rows = 1;
+  for (int64_t i = 0; i + 1 < x.dim(); ++i) rows *= x.size(i);
+  return inner(x.reshape({rows, x.size(-1)}));
+}
+
+std::vector<int64_t> out_shape(const Tensor& x, int64_t n) {
+  std::vector<int64_t> s(x.sizes().begin(), x.sizes().end());
+  s.back() = n;
+  return s;
+}
+
+void linear_call(const Tensor& x2, const Tensor& weight, const c10::optional<Tensor>& bias,
+                 const Tensor& y2, const at::Device& dev) {
+  const Tensor w = inner(weight);
+  const Tensor b = bias ? inner(*bias) : Tensor();
+  c10::DeviceGuard guard(dev);
+  cea_tensor a = arg(x2), c = arg(w), e = arg(y2);
+  if (b.defined()) {
+    cea_tensor d = arg(b);
+    check_rc(cea_linear(&a, &c, &d, &e, stream_of(dev)), "linear");
+  } else {
+    check_rc(cea_linear(&a, &c, nullptr, &e, stream_of(dev)), "linear");
+  }
+}
+
+Tensor linear(const Tensor& x, const Tensor& weight, const c10::optional<Tensor>& bias) {
+  const Tensor bd = bias ? *bias : Tensor();
+  const at::Device dev = device_of({&x, &weight, &bd});
+  TORCH_CHECK_VALUE(weight.dim() == 2, "weight must be [out_features, in_features]");
+  const Tensor x2 = rows_of(x);
+  Tensor y = at::empty(out_shape(x, weight.size(0)), x.options());
+  linear_call(x2, weight, bias, y.view({x2.size(0), weight.size(0)}), dev);
+  return y;
+}
+
+// y: a preallocated [M, N] buffer (any row stride, innermost stride 1)
+void linear_into(Tensor y, const Tensor& x, const Tensor& weight, const c10::optional<Tensor>& bias) {
+  const Tensor bd = bias ? *bias : Tensor();
+  const at::Device dev = device_of({&y, &x, &weight, &bd});
+  TORCH_CHECK_VALUE(weight.dim() == 2, "weight must be [out_features, in_features]");
+  TORCH_CHECK_VALUE(y.dim() == 2, "out must be 2-D [rows, out_features]");
+  TORCH_CHECK_VALUE(y.size(-1) <= 1 || y.stride(-1) == 1, "out must have innermost stride 1");
+  linear_call(rows_of(x), weight, bias, y, dev);
+}
+
+Tensor linear_gated(const Tensor& x, const Tensor& w_gate, const Tensor& w_up,
+                    const c10::optional<Tensor>& b_gate, const c10::optional<Tensor>& b_up, int64_t act) {
+  const Tensor bg = b_gate ? inner(*b_gate) : Tensor(), bu = b_up ? inner(*b_up) : Tensor();
+  const at::Device dev = device_of({&x, &w_gate, &w_up, &bg, &bu});
+  TORCH_CHECK_VALUE(w_gate.dim() == 2 && w_up.dim() == 2, "weights must be [units, in_features]");
+  const Tensor x2 = rows_of(x);
+  Tensor wg = inner(w_gate), wu = inner(w_up);
+  if (wg.size(0) > 1 && wu.stride(0) != wg.stride(0)) {
+    wg = wg.contiguous();
+    wu = wu.contiguous();
+  }
+  Tensor y = at::empty(out_shape(x, w_gate.size(0)), x.options());
+  c10::DeviceGuard guard(dev);
+  cea_tensor a = arg(x2), c = arg(wg), d = arg(wu), e = arg(y.view({x2.size(0), w_gate.size(0)}));
+  cea_tensor f, g;
+  if (bg.defined()) f = arg(bg);
+  if (bu.defined()) g = arg(bu);
+  check_rc(cea_linear_gated(&a, &c, &d, bg.defined() ? &f : nullptr, bu.defined() ? &g : nullptr, &e,
+                            (int32_t)act, stream_of(dev)),
+           "linear_gated");
+  return y;
+}
+
 void kv_append(Tensor cache_k, Tensor cache_v, Tensor cache_pos, int64_t offset, const Tensor& k_in,
                const Tensor& v_in, const Tensor& pos_in, c10::optional<Tensor> cos_in,
                c10::optional<Tensor> sin_in) {
@@ -419,6 +490,9 @@ TORCH_LIBRARY(collab_edge, m) {
   m.def("rmsnorm_rope(Tensor x, Tensor weight, float eps, Tensor positions, Tensor inv_freq, int num_heads) "
         "-> Tensor");
   m.def("gated_mul(Tensor gate, Tensor up, int act) -> Tensor");
+  m.def("linear(Tensor x, Tensor weight, Tensor? bias) -> Tensor");
+  m.def("linear_into(Tensor(a!) out, Tensor x, Tensor weight, Tensor? bias) -> ()");
+  m.def("linear_gated(Tensor x, Tensor w_gate, Tensor w_up, Tensor? b_gate, Tensor? b_up, int act) -> Tensor");
   m.def("kv_append(Tensor(a!) cache_k, Tensor(b!) cache_v, Tensor(c!) cache_pos, int offset, Tensor k, "
         "Tensor v, Tensor pos, Tensor? cos, Tensor? sin) -> ()");
 }
@@ -437,5 +511,8 @@ TORCH_LIBRARY_IMPL(collab_edge, CompositeExplicitAutograd, m) {
   m.impl("apply_rotary", apply_rotary);
   m.impl("rmsnorm_rope", rmsnorm_rope);
   m.impl("gated_mul", gated_mul);
+  m.impl("linear", linear);
+  m.impl("linear_into", linear_into);
+  m.impl("linear_gated", linear_gated);
   m.impl("kv_append", kv_append);
 }

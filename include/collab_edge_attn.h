@@ -294,6 +294,36 @@ int cea_silu_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, 
 int cea_gated_mul(const cea_tensor* gate, const cea_tensor* up, cea_tensor* out, int32_t act,
                   void* stream);
 
+/*
+ * Fused column-parallel projection: y = x . weight^T (+ bias), one GEMM for all the
+ * projections that share the input (Q/K/V, gate/up), f32 accumulation (f64 for f64) rounded
+ * once to the input dtype.  Replaces F.linear(x, self.weight, self.bias) of
+ * FusedColumnParallelLinear (collab_infer/parallel/tensor_parallel.py:294-295); the
+ * per-projection outputs of .split(local_sizes, dim=-1) are column views of y.
+ *   x [M, K], weight [N, K], bias [N] or NULL, y [M, N]: one dtype (bf16 / f16 / f32 / f64),
+ *   innermost stride 1, any row strides (rows must not overlap); y must not overlap x, weight
+ *   or bias.  bf16 / f16 with K, both row strides a multiple of 8 and 16-byte aligned x and
+ *   weight run on the matrix cores; everything else on a generic kernel.
+ */
+int cea_linear(const cea_tensor* x, const cea_tensor* weight, const cea_tensor* bias,
+               cea_tensor* y, void* stream);
+
+/*
+ * The gated MLP's gate/up projection and its activation in one pass:
+ *   gate = x . w_gate^T + b_gate,  up = x . w_up^T + b_up  (each rounded to the input dtype),
+ *   y = act(gate) * up  with act(gate) rounded first,
+ * without the [M, 2I] gate/up intermediate.  Replaces `gate, up = self.gate_up_proj(x);
+ * h = self.act(gate) * up` of the gated MLP (collab_infer/models/llama.py:302-305, the fused
+ * GEMM of tensor_parallel.py:294-295) and the two F.linear calls and activation of its
+ * replicated-token branch (llama.py:309-316).
+ *   x [M, K]; w_gate, w_up [I, K] with one row stride (e.g. the two halves, or any two row
+ *   ranges, of the fused [2I, K] parameter); b_gate, b_up [I] (both or neither); y [M, I];
+ *   act one of CEA_ACT_*.  Dtypes and paths as cea_linear.
+ */
+int cea_linear_gated(const cea_tensor* x, const cea_tensor* w_gate, const cea_tensor* w_up,
+                     const cea_tensor* b_gate, const cea_tensor* b_up, cea_tensor* y,
+                     int32_t act, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,7 +15,8 @@ def test_header_lists_the_entry_points(cea):
     names = cea._native.header_symbols()
     for expected in ("cea_attention_with_lse", "cea_merge_attention", "cea_merge_attention_list",
                      "cea_partitioned_attention", "cea_rmsnorm", "cea_rope_tables",
-                     "cea_apply_rotary", "cea_rmsnorm_rope", "cea_silu_mul", "cea_last_error"):
+                     "cea_apply_rotary", "cea_rmsnorm_rope", "cea_silu_mul", "cea_linear",
+                     "cea_linear_gated", "cea_last_error"):
         assert expected in names
 
 
@@ -111,6 +112,38 @@ def test_layer_ops_reject_bad_shapes(cea):
     assert rc == nat.EINVAL
 
 
+def test_projection_rejects_bad_arguments(cea):
+    """cea_linear / cea_linear_gated validate shapes, dtypes and the activation before any
+    launch (the pointers here are never dereferenced)."""
+    nat = cea._native
+    lib = nat.load_library()
+    bf16, i64 = 1, 4
+    x, w, y = _t((4, 8), bf16), _t((5, 7), bf16), _t((4, 5), bf16)
+    rc = lib.cea_linear(ctypes.byref(x), ctypes.byref(w), None, ctypes.byref(y), None)
+    assert rc == nat.EINVAL and "input features" in nat.last_error()
+    w = _t((5, 8), bf16)
+    b = _t((4,), bf16)
+    rc = lib.cea_linear(ctypes.byref(x), ctypes.byref(w), ctypes.byref(b), ctypes.byref(y), None)
+    assert rc == nat.EINVAL and "bias" in nat.last_error()
+    y6 = _t((4, 6), bf16)
+    rc = lib.cea_linear(ctypes.byref(x), ctypes.byref(w), None, ctypes.byref(y6), None)
+    assert rc == nat.EINVAL and "y must be" in nat.last_error()
+    xi, wi, yi = _t((4, 8), i64), _t((5, 8), i64), _t((4, 5), i64)
+    rc = lib.cea_linear(ctypes.byref(xi), ctypes.byref(wi), None, ctypes.byref(yi), None)
+    assert rc == nat.EUNSUPPORTED
+    wu = _t((6, 8), bf16)
+    rc = lib.cea_linear_gated(ctypes.byref(x), ctypes.byref(w), ctypes.byref(wu), None, None,
+                              ctypes.byref(y), 0, None)
+    assert rc == nat.EINVAL and "same number of rows" in nat.last_error()
+    rc = lib.cea_linear_gated(ctypes.byref(x), ctypes.byref(w), ctypes.byref(w), None, None,
+                              ctypes.byref(y), 9, None)
+    assert rc == nat.EUNSUPPORTED and "activation" in nat.last_error()
+    bg = _t((5,), bf16)
+    rc = lib.cea_linear_gated(ctypes.byref(x), ctypes.byref(w), ctypes.byref(w), ctypes.byref(bg),
+                              None, ctypes.byref(y), 0, None)
+    assert rc == nat.EINVAL and "both biases" in nat.last_error()
+
+
 def test_python_api_refuses_host_tensors(cea):
     q = torch.zeros(1, 2, 2, 8, dtype=torch.bfloat16)
     p = torch.arange(2).view(1, 2)
@@ -134,7 +167,7 @@ def test_python_api_validates_heads_before_device_work(cea):
 
 OPS = ["attention", "attention_into", "merge", "partitioned", "pack_partial", "merge_packed",
        "ulysses_scatter", "ulysses_gather", "rmsnorm", "rope_tables", "apply_rotary",
-       "rmsnorm_rope", "gated_mul", "kv_append"]
+       "rmsnorm_rope", "gated_mul", "kv_append", "linear", "linear_into", "linear_gated"]
 
 
 def test_torch_operator_library_registers_every_op(cea):
@@ -147,7 +180,7 @@ def test_torch_operator_library_registers_every_op(cea):
     # the package's functions go through these operators, not through ctypes
     import inspect
 
-    for mod in (cea.attention, cea.layers, cea.sequence_parallel, cea.kv_cache):
+    for mod in (cea.attention, cea.layers, cea.sequence_parallel, cea.kv_cache, cea.projection):
         src = inspect.getsource(mod)
         assert "nat.ops()" in src and "byref" not in src, mod.__name__
 
@@ -161,6 +194,10 @@ def test_operators_refuse_host_tensors(cea):
         ops.attention(q, q, q, pos, pos, True, 0.35, None, True)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.gated_mul(q.view(4, 16), q.view(4, 16), 0)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.linear(q.view(4, 16), q.view(4, 16), None)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        cea.projection.linear_gated(q.view(4, 16), q.view(4, 16), q.view(4, 16))
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         cea.attention_with_lse(q, q, q, pos, pos)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
