@@ -17,13 +17,14 @@
 //   * the MFMA's A operand is the weight (32 rows) and B the tokens (32 columns), so 4
 //     consecutive accumulator values of a lane are 4 consecutive output features of one
 //     token, stored as one 8-byte access;
-//   * 32-wide K slices of both operands go global -> LDS directly (buffer_load ... lds)
-//     through a 4-stage ring with 3 slices in flight; the 64-byte rows of a slice are
+//   * 64-wide K slices of both operands go global -> LDS directly (buffer_load ... lds) into
+//     two LDS stages, the next slice loading while the current one is multiplied; a slice
+//     row is one 128-byte cache line, so every L2 request moves a whole line; rows are
 //     XOR-swizzled in 16-byte groups so that the fragment reads (ds_read_b128) of any 8 or 16
 //     consecutive lanes hit distinct banks;
-//   * one barrier per slice, between its two 16-wide halves: it publishes the next slice and
+//   * one barrier per slice, before its last 16-wide step: it publishes the next slice and
 //     frees the buffer just read, which the wave refills at once; the fragments of the next
-//     half are read while the matrix cores work on the current one;
+//     step are read while the matrix cores work on the current one;
 //   * rows past M / N and columns past K read as zero through the buffer resources' range
 //     check, so ragged tiles take no branches in the loop;
 //   * workgroups are dealt to the 8 XCDs round robin; tiles are renumbered so that each XCD
@@ -59,15 +60,16 @@ enum { kPlain = 0, kGated = 1 };
 constexpr int G_THREADS = 256;
 constexpr int G_BM = 256;                            // tokens per tile
 constexpr int G_BW = 256;                            // weight rows per tile
-constexpr int G_BK = 32;                             // K per LDS slice
-constexpr int G_ROW = G_BK * 2;                      // bytes of one row of a slice
-constexpr int G_NST = 4;                             // LDS ring depth
-constexpr int G_OPER = G_BM * G_ROW;                 // 16 KB per operand per slice
+constexpr int G_BK = 64;                             // K per LDS slice
+constexpr int G_ROW = G_BK * 2;                      // bytes of one row of a slice: a cache line
+constexpr int G_NST = 2;                             // LDS stages
+constexpr int G_OPER = G_BM * G_ROW;                 // 32 KB per operand per slice
 constexpr int G_STAGE = 2 * G_OPER;                  // weight slice, then token slice
 constexpr int G_LDS = G_NST * G_STAGE;               // 128 KB
 constexpr int G_LOADS = G_OPER / (G_THREADS * 16);   // 16-byte loads per lane per operand
 constexpr uint32_t kOutOfRange = 0x80000000u;        // above every resource's range
-static_assert(G_LOADS == 4 && G_BM == G_BW, "the load pattern assumes 4 x 16 rows per wave");
+constexpr int kLgkm0 = 0xC07F;   // s_waitcnt lgkmcnt(0), vmcnt / expcnt left at their maximum
+static_assert(G_LOADS == 8 && G_BM == G_BW, "the load pattern assumes 8 x 8 rows per wave");
 
 struct GemmParams {
   const void* x;    // [M, K], row stride ldx
@@ -79,16 +81,14 @@ struct GemmParams {
   int64_t ldx, ldw, ldy;
   int32_t M, N, K;  // N = output columns
   int32_t tiles_m, tiles_n, group_m;
-  int32_t vec_out;  // y takes 4-element stores at every 4th column
+  int32_t vec_out;  // 2: 16-byte row chunks, 1: 4-element stores, 0: element stores
 };
 
-// 16-byte group swizzle of a slice row: group c of row r sits at group c ^ g_swz(r).  Any 8
-// consecutive rows (fixed r & 1) and any 16 consecutive rows (fixed r & 3) get distinct
-// values, so 8-lane groups read distinct 16-byte bank groups within 128 bytes and 16-lane
-// groups within 256 bytes.
-__device__ __forceinline__ int g_swz(int r) {
-  return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) << 1);
-}
+// 16-byte group swizzle of a slice row (8 groups of 16 bytes): group c of row r sits at group
+// c ^ g_swz(r).  Any 8 consecutive rows get distinct values, and so do the 8 rows of either
+// parity among 16 consecutive rows, so 8-lane groups of a fragment read hit distinct 16-byte
+// bank groups within 128 bytes and 16-lane groups within 256 bytes.  Depends on r & 15 only.
+__device__ __forceinline__ int g_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // Tile (token block, weight block) of this workgroup.
 __device__ __forceinline__ void tile_of(const GemmParams& p, int& tm, int& tn) {
@@ -202,22 +202,22 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
                    (uint32_t)((int64_t)(rows - 1) * p.ldw * ESZ + (int64_t)K * ESZ));
   }
 
-  // Slice loads: wave w fills rows [64w, 64w + 64) of both operands, 16 rows per load; lane l
-  // brings 16-byte group (l & 3) ^ g_swz(row) of row 64w + 16i + (l >> 2) to group l & 3.
-  // The per-lane offsets stay fixed; the slice's K offset is the scalar soffset.
-  const int lrow = lane >> 2;
-  const int grp = (lane & 3) ^ g_swz(lrow);   // g_swz(row) only depends on row & 15
-  const int kcol = grp * 8;                   // first element column of the group in a slice
+  // Slice loads: wave w fills rows [64w, 64w + 64) of both operands, 8 rows x 128 bytes per
+  // instruction; lane l brings 16-byte group
+  // (l & 7) ^ g_swz(row) of row 64w + 8i + (l >> 3) to group l & 7.  The per-lane offsets
+  // stay fixed; the slice's K offset is the scalar soffset.
   uint32_t off_w[G_LOADS], off_x[G_LOADS];
+  int kcol[2];   // first element column of the lane's group in a slice, for even / odd i
 #pragma unroll
   for (int i = 0; i < G_LOADS; ++i) {
-    const int row = 64 * wave + 16 * i + lrow;
+    const int row = 64 * wave + 8 * i + (lane >> 3);
+    const int grp = (lane & 7) ^ g_swz(row);
+    if (i < 2) kcol[i] = grp * 8;
     const int wrow = MODE == kGated ? (row & 127) : row;
     off_w[i] = (uint32_t)((int64_t)wrow * p.ldw * ESZ) + grp * 16;
     off_x[i] = (uint32_t)((int64_t)row * p.ldx * ESZ) + grp * 16;
   }
-  const uint32_t lds0 = lds_addr(smem);
-  const uint32_t lds_wave = lds0 + wave * G_LOADS * 1024;
+  const uint32_t lds_wave = lds_addr(smem) + wave * G_LOADS * 1024;
   auto issue = [&](int s) {
     const uint32_t sb = lds_wave + (uint32_t)(s & (G_NST - 1)) * G_STAGE;
     const uint32_t kb = (uint32_t)s * G_ROW;
@@ -228,23 +228,25 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
       for (int i = 0; i < G_LOADS; ++i)
         buffer_load_lds16_m0_so(rx, sb + G_OPER + i * 1024, off_x[i], kb);
     } else {   // K tail: groups past K read as zero
-      const bool kin = s * G_BK + kcol < K;
+      const bool kin0 = s * G_BK + kcol[0] < K, kin1 = s * G_BK + kcol[1] < K;
 #pragma unroll
       for (int i = 0; i < G_LOADS; ++i)
-        buffer_load_lds16_m0_so(rw, sb + i * 1024, kin ? off_w[i] : kOutOfRange, kb);
+        buffer_load_lds16_m0_so(rw, sb + i * 1024, ((i & 1) ? kin1 : kin0) ? off_w[i] : kOutOfRange, kb);
 #pragma unroll
       for (int i = 0; i < G_LOADS; ++i)
-        buffer_load_lds16_m0_so(rx, sb + G_OPER + i * 1024, kin ? off_x[i] : kOutOfRange, kb);
+        buffer_load_lds16_m0_so(rx, sb + G_OPER + i * 1024,
+                                ((i & 1) ? kin1 : kin0) ? off_x[i] : kOutOfRange, kb);
     }
   };
 
   // Fragment reads: lane l takes row (l & 31) of a 32-row block, elements 8 * (l >> 5) .. +8
-  // of the 16-wide half h of the slice, i.e. group 2h + (l >> 5).
+  // of the 16-wide step q of the slice, i.e. group 2q + (l >> 5).
   const int fr = lane & 31;
-  const uint32_t rd0 = fr * G_ROW + (((0 + (lane >> 5)) ^ g_swz(fr)) << 4);
-  const uint32_t rd1 = fr * G_ROW + (((2 + (lane >> 5)) ^ g_swz(fr)) << 4);
-  auto read = [&](int s, int half, frag (&fa)[4], frag (&fb)[4]) {
-    const char* sb = smem + (s & (G_NST - 1)) * G_STAGE + (half ? rd1 : rd0);
+  uint32_t rd[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) rd[q] = fr * G_ROW + (((2 * q + (lane >> 5)) ^ g_swz(fr)) << 4);
+  auto read = [&](int s, int q, frag (&fa)[4], frag (&fb)[4]) {
+    const char* sb = smem + (s & (G_NST - 1)) * G_STAGE + rd[q];
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
       const int arow = MODE == kGated ? (f >> 1) * 128 + wn * 64 + (f & 1) * 32 : wn * 128 + f * 32;
@@ -267,8 +269,8 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[f][t] = GMfma<T>::run(fa[f], fb[t], acc[f][t]);
   };
-  // schedule of a half step: the 8 fragment reads of the next half go out one after each of
-  // the first 8 matrix instructions, so they have the rest of the half to land
+  // schedule of a 16-wide step: the 8 fragment reads of the next step go out one after each
+  // of the first 8 matrix instructions, so they have the rest of the step to land
   auto interleave = [&]() {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -276,51 +278,48 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-  };
-  // waits for this wave's loads of a slice, given how many slices it issued after that one
-  auto wait_slice = [&](int after) {
-    if (after >= 3) wait_vmcnt<3 * 2 * G_LOADS>();
-    else if (after == 2) wait_vmcnt<2 * 2 * G_LOADS>();
-    else if (after == 1) wait_vmcnt<2 * G_LOADS>();
-    else wait_vmcnt<0>();
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  frag a0[4], b0[4], a1[4], b1[4];
-  const int pre = KT < G_NST ? KT : G_NST;
-  for (int s = 0; s < pre; ++s) issue(s);
+  // Two stages: slice s + 1 loads while slice s is multiplied.  One barrier per slice, before
+  // its last 16-wide step: by then every wave has read all of slice s (its buffer can be
+  // refilled with slice s + 2) and slice s + 1 has landed (its first fragments can be read).
+  frag fa0[4], fb0[4], fa1[4], fb1[4];
+  if (KT > 0) issue(0);
+  if (KT > 1) issue(1);
   if (KT > 0) {
-    wait_slice(pre - 1);
+    if (KT > 1) wait_vmcnt<2 * G_LOADS>();
+    else wait_vmcnt<0>();
     barrier_no_fence();
-    read(0, 0, a0, b0);
+    read(0, 0, fa0, fb0);
   }
-  int kt = 0;
-  // steady state: slice kt + G_NST exists and goes into the buffer of slice kt
-  for (; kt + G_NST < KT; ++kt) {
-    read(kt, 1, a1, b1);
-    mma(a0, b0);
+  // the first three 16-wide steps of slice s, reading the fragments of the next step
+  auto steps012 = [&](int s) {
+    read(s, 1, fa1, fb1);
+    mma(fa0, fb0);
     interleave();
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<2 * 2 * G_LOADS>();   // slice kt + 1 is in (kt + 2, kt + 3 may be in flight)
-    wait_lgkmcnt0();                 // this wave's reads of slice kt are done
+    read(s, 2, fa0, fb0);
+    mma(fa1, fb1);
+    interleave();
+    read(s, 3, fa1, fb1);
+    mma(fa0, fb0);
+    interleave();
+  };
+  int s = 0;
+  for (; s + 1 < KT; ++s) {
+    steps012(s);
+    wait_vmcnt<0>();                    // slice s + 1 is in
+    __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's reads of slice s are done
     barrier_no_fence();
-    issue(kt + G_NST);
+    if (s + 2 < KT) issue(s + 2);
     __builtin_amdgcn_sched_barrier(0);
-    read(kt + 1, 0, a0, b0);
-    mma(a1, b1);
+    read(s + 1, 0, fa0, fb0);
+    mma(fa1, fb1);
     interleave();
-    __builtin_amdgcn_sched_barrier(0);
   }
-  // last slices: everything is issued
-  for (; kt < KT; ++kt) {
-    read(kt, 1, a1, b1);
-    mma(a0, b0);
-    if (kt + 1 < KT) {
-      wait_slice(KT - 2 - kt);
-      wait_lgkmcnt0();
-      barrier_no_fence();
-      read(kt + 1, 0, a0, b0);
-    }
-    mma(a1, b1);
+  if (KT > 0) {   // last slice
+    steps012(s);
+    mma(fa1, fb1);
   }
 
   // epilogue: lane (t, g) holds token column t of every 32 x 32 block and, per accumulator
@@ -330,6 +329,60 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
   const bool vec = p.vec_out != 0;
   T* y = (T*)p.y;
   constexpr int NF = MODE == kGated ? 2 : 4;   // output column blocks per wave
+  if (p.vec_out == 2) {
+    // Staged through LDS (free once every wave has read its last fragments): each wave
+    // writes its 128 x NCOL output block into its own LDS region, then stores whole rows,
+    // 16 bytes per lane, so every cache line of y is written by one instruction.
+    constexpr int NCOL = NF * 32;          // output columns of a wave
+    constexpr int RB = NCOL * 2;           // bytes of a staged row
+    constexpr int CPR = RB / 16;           // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;          // rows per store instruction
+    // chunk swizzle of a staged row: the 16 (or 8 pairs of) rows one write instruction
+    // touches spread over distinct bank groups
+    auto row_swz = [](int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); };
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+    barrier_no_fence();
+    char* stage = smem + wave * (128 * RB);
+    const int col0 = n0 + wn * NCOL;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int col = col0 + f * 32 + 8 * i + 4 * g;
+        float bgv[4], buv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        bias4<T, float>(p.bg, col, p.N, true, bgv);
+        if constexpr (MODE == kGated) bias4<T, float>(p.bu, col, p.N, true, buv);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float gv[4], uv[4], v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            gv[j] = acc[f][t][4 * i + j];
+            uv[j] = MODE == kGated ? acc[f + 2][t][4 * i + j] : 0.0f;
+          }
+          finish4<T, MODE, ACT, float>(gv, uv, bgv, buv, v);
+          T o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = store_cast<T, float>(v[j]);
+          uint2 raw;
+          __builtin_memcpy(&raw, o, 8);
+          const int row = t * 32 + (lane & 31);
+          const int chunk = (4 * f + i) ^ row_swz(row);
+          *(uint2*)(stage + row * RB + chunk * 16 + g * 8) = raw;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 128 / RPI; ++k) {
+      const int row = k * RPI + lane / CPR;
+      const int c = lane % CPR;
+      const uint4 raw = *(const uint4*)(stage + row * RB + ((c ^ row_swz(row)) * 16));
+      const int tok = m0 + wm * 128 + row;
+      const int col = col0 + c * 8;
+      if (tok < p.M && col < p.N) *(uint4*)(y + (int64_t)tok * p.ldy + col) = raw;
+    }
+    return;
+  }
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
 #pragma unroll
@@ -523,11 +576,13 @@ int launch_linear(const cea_tensor* x, const cea_tensor* wg, const cea_tensor* w
   p.ldx = x->size[0] > 1 ? x->stride[0] : p.K;
   p.ldw = wg->size[0] > 1 ? wg->stride[0] : p.K;
   p.ldy = y->size[0] > 1 ? y->stride[0] : p.N;
-  p.vec_out = (p.N % 4 == 0 && p.ldy % 4 == 0 && ((uintptr_t)p.y & 7) == 0 &&
-               (p.bg == nullptr || ((uintptr_t)p.bg & 7) == 0) &&
-               (p.bu == nullptr || ((uintptr_t)p.bu & 7) == 0))
-                  ? 1
-                  : 0;
+  // output stores: 2 = whole 16-byte chunks staged through LDS, 1 = 8-byte stores,
+  // 0 = element stores
+  const bool v8 = p.N % 4 == 0 && p.ldy % 4 == 0 && ((uintptr_t)p.y & 7) == 0 &&
+                  (p.bg == nullptr || ((uintptr_t)p.bg & 7) == 0) &&
+                  (p.bu == nullptr || ((uintptr_t)p.bu & 7) == 0);
+  const bool v16 = v8 && p.N % 8 == 0 && p.ldy % 8 == 0 && ((uintptr_t)p.y & 15) == 0;
+  p.vec_out = v16 ? 2 : v8 ? 1 : 0;
   if (p.M == 0 || p.N == 0) return CEA_OK;
   const bool mfma = mfma_path(p, x->dtype, mode);
   switch (x->dtype) {
