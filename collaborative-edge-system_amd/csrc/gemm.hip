@@ -12,25 +12,28 @@
 //
 // Matrix-core kernel (bf16 / f16, 16-byte aligned rows, K a multiple of 8):
 //   * one workgroup = 4 waves, one per SIMD (512 registers each), computes 256 tokens x 256
-//     weight rows; each wave owns a 128 x 128 block whose 16 accumulators of
-//     v_mfma_f32_32x32x16 (256 registers) live in the accumulation registers throughout;
-//   * the MFMA's A operand is the weight (32 rows) and B the tokens (32 columns), so 4
-//     consecutive accumulator values of a lane are 4 consecutive output features of one
-//     token, stored as one 8-byte access;
-//   * 64-wide K slices of both operands go global -> LDS directly (buffer_load ... lds) into
-//     two LDS stages, the next slice loading while the current one is multiplied; a slice
-//     row is one 128-byte cache line, so every L2 request moves a whole line; rows are
-//     XOR-swizzled in 16-byte groups so that the fragment reads (ds_read_b128) of any 8 or 16
-//     consecutive lanes hit distinct banks;
-//   * one barrier per slice, before its last 16-wide step: it publishes the next slice and
-//     frees the buffer just read, which the wave refills at once; the fragments of the next
-//     step are read while the matrix cores work on the current one;
+//     weight rows; each wave owns a 128 x 128 block whose 64 accumulators of
+//     v_mfma_f32_16x16x32 (256 registers) live in the accumulation registers throughout;
+//   * the MFMA's A operand is the weight (16 rows) and B the tokens (16 columns), so the 4
+//     accumulator values of a lane are 4 consecutive output features of one token;
+//   * 32-wide K slices of both operands go global -> LDS directly (buffer_load ... lds)
+//     through a 4-buffer ring, 3 slices ahead of the one being multiplied; the 64-byte rows
+//     of a slice are XOR-swizzled in 16-byte groups so that the fragment reads
+//     (ds_read_b128) of any 8 or 16 consecutive lanes hit distinct banks;
+//   * one barrier per slice; the slice's 64 matrix instructions each carry a share of the
+//     rest: the 16 fragment reads of the next slice (one per 4) and the 8 loads that refill
+//     the buffer just freed (one per 8), so neither the LDS nor the address unit sees a burst
+//     that would hold every wave at once;
 //   * rows past M / N and columns past K read as zero through the buffer resources' range
 //     check, so ragged tiles take no branches in the loop;
+//   * the output block goes through LDS and leaves as whole 16-byte row chunks, so each
+//     cache line of y is written by one store instruction;
 //   * workgroups are dealt to the 8 XCDs round robin; tiles are renumbered so that each XCD
 //     works through a compact group of tiles that share operand rows in its L2.
 // Generic kernel (any dtype, stride or alignment): LDS-tiled FMA loop with f32 accumulation
 // (f64 for f64 tensors).
+#include <type_traits>
+
 #include "cea_kernels.hpp"
 #include "cea_lds_dma.hpp"
 
@@ -39,19 +42,19 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T> struct GMfma;
 template <> struct GMfma<bf16> {
   typedef bf16x8 frag;
-  static __device__ __forceinline__ f32x16 run(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  static __device__ __forceinline__ f32x4 run(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
 };
 template <> struct GMfma<f16> {
   typedef f16x8 frag;
-  static __device__ __forceinline__ f32x16 run(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  static __device__ __forceinline__ f32x4 run(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
 
@@ -60,16 +63,16 @@ enum { kPlain = 0, kGated = 1 };
 constexpr int G_THREADS = 256;
 constexpr int G_BM = 256;                            // tokens per tile
 constexpr int G_BW = 256;                            // weight rows per tile
-constexpr int G_BK = 64;                             // K per LDS slice
-constexpr int G_ROW = G_BK * 2;                      // bytes of one row of a slice: a cache line
-constexpr int G_NST = 2;                             // LDS stages
-constexpr int G_OPER = G_BM * G_ROW;                 // 32 KB per operand per slice
+constexpr int G_BK = 32;                             // K per LDS slice
+constexpr int G_ROW = G_BK * 2;                      // bytes of one row of a slice
+constexpr int G_NST = 4;                             // LDS ring depth
+constexpr int G_OPER = G_BM * G_ROW;                 // 16 KB per operand per slice
 constexpr int G_STAGE = 2 * G_OPER;                  // weight slice, then token slice
 constexpr int G_LDS = G_NST * G_STAGE;               // 128 KB
 constexpr int G_LOADS = G_OPER / (G_THREADS * 16);   // 16-byte loads per lane per operand
 constexpr uint32_t kOutOfRange = 0x80000000u;        // above every resource's range
 constexpr int kLgkm0 = 0xC07F;   // s_waitcnt lgkmcnt(0), vmcnt / expcnt left at their maximum
-static_assert(G_LOADS == 8 && G_BM == G_BW, "the load pattern assumes 8 x 8 rows per wave");
+static_assert(G_LOADS == 4 && G_BM == G_BW, "the load pattern assumes 4 x 16 rows per wave");
 
 struct GemmParams {
   const void* x;    // [M, K], row stride ldx
@@ -84,11 +87,14 @@ struct GemmParams {
   int32_t vec_out;  // 2: 16-byte row chunks, 1: 4-element stores, 0: element stores
 };
 
-// 16-byte group swizzle of a slice row (8 groups of 16 bytes): group c of row r sits at group
-// c ^ g_swz(r).  Any 8 consecutive rows get distinct values, and so do the 8 rows of either
-// parity among 16 consecutive rows, so 8-lane groups of a fragment read hit distinct 16-byte
-// bank groups within 128 bytes and 16-lane groups within 256 bytes.  Depends on r & 15 only.
-__device__ __forceinline__ int g_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// 16-byte group swizzle of a slice row (4 groups of 16 bytes): group c of row r sits at group
+// c ^ g_swz(r).  Among any 16 consecutive rows the 4 rows of equal r & 3 get distinct values,
+// and among any 8 consecutive rows the 4 of equal parity do, so the 16-lane groups of a
+// fragment read (16 rows, one group) hit distinct 16-byte bank groups within 256 bytes and
+// 8-lane groups within 128 bytes.  Depends on r & 15 only.
+__device__ __forceinline__ int g_swz(int r) {
+  return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) << 1);
+}
 
 // Tile (token block, weight block) of this workgroup.
 __device__ __forceinline__ void tile_of(const GemmParams& p, int& tm, int& tn) {
@@ -202,174 +208,152 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
                    (uint32_t)((int64_t)(rows - 1) * p.ldw * ESZ + (int64_t)K * ESZ));
   }
 
-  // Slice loads: wave w fills rows [64w, 64w + 64) of both operands, 8 rows x 128 bytes per
-  // instruction; lane l brings 16-byte group
-  // (l & 7) ^ g_swz(row) of row 64w + 8i + (l >> 3) to group l & 7.  The per-lane offsets
-  // stay fixed; the slice's K offset is the scalar soffset.
+  // Slice loads: wave w fills rows [64w, 64w + 64) of both operands, 16 rows x 64 bytes per
+  // instruction; lane l brings 16-byte group (l & 3) ^ g_swz(row) of row 64w + 16i + (l >> 2)
+  // to group l & 3 (g_swz(row) only depends on row & 15 = l >> 2).  The per-lane offsets
+  // stay fixed; the slice's K offset is the scalar soffset, and groups past K (the last
+  // slice of a K that is not a multiple of 32) get an offset past the resource's range.
+  const int grp = (lane & 3) ^ g_swz(lane >> 2);
+  const int kcol = grp * 8;   // first element column of the lane's group in a slice
   uint32_t off_w[G_LOADS], off_x[G_LOADS];
-  int kcol[2];   // first element column of the lane's group in a slice, for even / odd i
 #pragma unroll
   for (int i = 0; i < G_LOADS; ++i) {
-    const int row = 64 * wave + 8 * i + (lane >> 3);
-    const int grp = (lane & 7) ^ g_swz(row);
-    if (i < 2) kcol[i] = grp * 8;
+    const int row = 64 * wave + 16 * i + (lane >> 2);
     const int wrow = MODE == kGated ? (row & 127) : row;
     off_w[i] = (uint32_t)((int64_t)wrow * p.ldw * ESZ) + grp * 16;
     off_x[i] = (uint32_t)((int64_t)row * p.ldx * ESZ) + grp * 16;
   }
   const uint32_t lds_wave = lds_addr(smem) + wave * G_LOADS * 1024;
-  auto issue = [&](int s) {
+  // load i of slice s (i < G_LOADS: weight rows, else token rows)
+  auto issue_one = [&](int s, int i) {
     const uint32_t sb = lds_wave + (uint32_t)(s & (G_NST - 1)) * G_STAGE;
     const uint32_t kb = (uint32_t)s * G_ROW;
-    if ((s + 1) * G_BK <= K) {
-#pragma unroll
-      for (int i = 0; i < G_LOADS; ++i) buffer_load_lds16_m0_so(rw, sb + i * 1024, off_w[i], kb);
-#pragma unroll
-      for (int i = 0; i < G_LOADS; ++i)
-        buffer_load_lds16_m0_so(rx, sb + G_OPER + i * 1024, off_x[i], kb);
-    } else {   // K tail: groups past K read as zero
-      const bool kin0 = s * G_BK + kcol[0] < K, kin1 = s * G_BK + kcol[1] < K;
-#pragma unroll
-      for (int i = 0; i < G_LOADS; ++i)
-        buffer_load_lds16_m0_so(rw, sb + i * 1024, ((i & 1) ? kin1 : kin0) ? off_w[i] : kOutOfRange, kb);
-#pragma unroll
-      for (int i = 0; i < G_LOADS; ++i)
-        buffer_load_lds16_m0_so(rx, sb + G_OPER + i * 1024,
-                                ((i & 1) ? kin1 : kin0) ? off_x[i] : kOutOfRange, kb);
-    }
+    const bool kin = s * G_BK + kcol < K;
+    if (i < G_LOADS)
+      buffer_load_lds16_m0_so(rw, sb + i * 1024, kin ? off_w[i] : kOutOfRange, kb);
+    else
+      buffer_load_lds16_m0_so(rx, sb + G_OPER + (i - G_LOADS) * 1024,
+                              kin ? off_x[i - G_LOADS] : kOutOfRange, kb);
   };
 
-  // Fragment reads: lane l takes row (l & 31) of a 32-row block, elements 8 * (l >> 5) .. +8
-  // of the 16-wide step q of the slice, i.e. group 2q + (l >> 5).
-  const int fr = lane & 31;
-  uint32_t rd[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) rd[q] = fr * G_ROW + (((2 * q + (lane >> 5)) ^ g_swz(fr)) << 4);
-  auto read = [&](int s, int q, frag (&fa)[4], frag (&fb)[4]) {
-    const char* sb = smem + (s & (G_NST - 1)) * G_STAGE + rd[q];
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const int arow = MODE == kGated ? (f >> 1) * 128 + wn * 64 + (f & 1) * 32 : wn * 128 + f * 32;
-      fa[f] = *(const frag*)(sb + arow * G_ROW);
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) fb[t] = *(const frag*)(sb + G_OPER + (wm * 128 + t * 32) * G_ROW);
+  // Fragment reads (v_mfma_f32_16x16x32): lane l takes row (l & 15) of a 16-row block and
+  // its 8 elements of group l >> 4; blocks start at multiples of 16 rows, so the swizzled
+  // position only depends on the lane.  Fragment j < 8 is weight block j, j >= 8 token
+  // block j - 8.
+  const uint32_t rd = (lane & 15) * G_ROW + ((((lane >> 4)) ^ g_swz(lane & 15)) << 4);
+  auto frag_row = [&](int j) {   // first LDS row of fragment j inside a stage
+    if (j < 8)
+      return MODE == kGated ? (j >> 2) * 128 + wn * 64 + (j & 3) * 16 : wn * 128 + j * 16;
+    return G_BM + wm * 128 + (j - 8) * 16;   // token rows follow the 256 weight rows
+  };
+  auto read_one = [&](int s, int j, frag (&fa)[8], frag (&fb)[8]) {
+    const char* a = smem + (s & (G_NST - 1)) * G_STAGE + rd + frag_row(j) * G_ROW;
+    if (j < 8) fa[j] = *(const frag*)a;
+    else fb[j - 8] = *(const frag*)a;
   };
 
-  f32x16 acc[4][4];
+  f32x4 acc[8][8];
 #pragma unroll
-  for (int f = 0; f < 4; ++f)
+  for (int f = 0; f < 8; ++f)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[f][t][e] = 0.0f;
-  auto mma = [&](const frag (&fa)[4], const frag (&fb)[4]) {
+      for (int e = 0; e < 4; ++e) acc[f][t][e] = 0.0f;
+
+  // The 64 matrix instructions of slice s (fragments fa / fb), each followed by a share of
+  // the other work: the 16 fragment reads of slice s + 1 (one per 4 instructions, into
+  // na / nb) and the 8 loads of slice s + 4 into the buffer slice s leaves (one per 8), so
+  // neither the LDS nor the address unit ever sees a burst.
+  auto slice = [&](int s, const frag (&fa)[8], const frag (&fb)[8], frag (&na)[8], frag (&nb)[8]) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
+    for (int f = 0; f < 8; ++f)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[f][t] = GMfma<T>::run(fa[f], fb[t], acc[f][t]);
+      for (int t = 0; t < 8; ++t) {
+        const int i = f * 8 + t;
+        acc[f][t] = GMfma<T>::run(fa[f], fb[t], acc[f][t]);
+        if ((i & 3) == 0) read_one(s + 1, i >> 2, na, nb);
+        if ((i & 7) == 4) issue_one(s + G_NST, i >> 3);
+        __builtin_amdgcn_sched_barrier(0);
+      }
   };
-  // schedule of a 16-wide step: the 8 fragment reads of the next step go out one after each
-  // of the first 8 matrix instructions, so they have the rest of the step to land
-  auto interleave = [&]() {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  // The barrier before slice s: slice s + 1 has landed for every wave (this wave issued
+  // slices s + 2 and s + 3 after it), and every wave has read all of slice s, whose buffer
+  // slice s refills.
+  auto sync = [&]() {
+    wait_vmcnt<2 * 2 * G_LOADS>();
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+    barrier_no_fence();
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Two stages: slice s + 1 loads while slice s is multiplied.  One barrier per slice, before
-  // its last 16-wide step: by then every wave has read all of slice s (its buffer can be
-  // refilled with slice s + 2) and slice s + 1 has landed (its first fragments can be read).
-  frag fa0[4], fb0[4], fa1[4], fb1[4];
-  if (KT > 0) issue(0);
-  if (KT > 1) issue(1);
-  if (KT > 0) {
-    if (KT > 1) wait_vmcnt<2 * G_LOADS>();
-    else wait_vmcnt<0>();
-    barrier_no_fence();
-    read(0, 0, fa0, fb0);
+  // Slices at or past KT are loaded with every offset out of range, i.e. as zeros: the loop
+  // runs uniformly (always 3 slices ahead, always reading the next slice), and the extra slice
+  // that rounds KT up to an even count adds exact zeros.
+  frag fa0[8], fb0[8], fa1[8], fb1[8];
+#pragma unroll
+  for (int s = 0; s < G_NST; ++s)
+#pragma unroll
+    for (int i = 0; i < 2 * G_LOADS; ++i) issue_one(s, i);
+  wait_vmcnt<3 * 2 * G_LOADS>();
+  barrier_no_fence();
+#pragma unroll
+  for (int j = 0; j < 16; ++j) read_one(0, j, fa0, fb0);
+  for (int s = 0; s < KT; s += 2) {   // two slices per trip: the fragment sets alternate
+    sync();
+    slice(s, fa0, fb0, fa1, fb1);
+    sync();
+    slice(s + 1, fa1, fb1, fa0, fb0);
   }
-  // the first three 16-wide steps of slice s, reading the fragments of the next step
-  auto steps012 = [&](int s) {
-    read(s, 1, fa1, fb1);
-    mma(fa0, fb0);
-    interleave();
-    read(s, 2, fa0, fb0);
-    mma(fa1, fb1);
-    interleave();
-    read(s, 3, fa1, fb1);
-    mma(fa0, fb0);
-    interleave();
-  };
-  int s = 0;
-  for (; s + 1 < KT; ++s) {
-    steps012(s);
-    wait_vmcnt<0>();                    // slice s + 1 is in
-    __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's reads of slice s are done
-    barrier_no_fence();
-    if (s + 2 < KT) issue(s + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    read(s + 1, 0, fa0, fb0);
-    mma(fa1, fb1);
-    interleave();
-  }
-  if (KT > 0) {   // last slice
-    steps012(s);
-    mma(fa1, fb1);
-  }
+  wait_vmcnt<0>();   // the last refills (zeros) land before the LDS is used again
 
-  // epilogue: lane (t, g) holds token column t of every 32 x 32 block and, per accumulator
-  // quad i, 4 consecutive weight rows 8i + 4g .. + 3
-  const int g = lane >> 5;
-  const int tok0 = m0 + wm * 128 + (lane & 31);
+  // epilogue: block (f, t) holds, in lane l, token column t * 16 + (l & 15) and the 4
+  // consecutive weight rows f * 16 + 4 * (l >> 4) .. + 3
+  const int q4 = lane >> 4;
   const bool vec = p.vec_out != 0;
   T* y = (T*)p.y;
-  constexpr int NF = MODE == kGated ? 2 : 4;   // output column blocks per wave
+  constexpr int NF = MODE == kGated ? 4 : 8;   // output column blocks of 16 per wave
+  constexpr int NCOL = NF * 16;                // output columns of a wave
+  const int col0 = n0 + wn * NCOL;
+  auto values = [&](int f, int t, const float (&bgv)[4], const float (&buv)[4], float (&v)[4]) {
+    float gv[4], uv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      gv[j] = acc[f][t][j];
+      uv[j] = MODE == kGated ? acc[f + 4][t][j] : 0.0f;
+    }
+    finish4<T, MODE, ACT, float>(gv, uv, bgv, buv, v);
+  };
   if (p.vec_out == 2) {
     // Staged through LDS (free once every wave has read its last fragments): each wave
     // writes its 128 x NCOL output block into its own LDS region, then stores whole rows,
     // 16 bytes per lane, so every cache line of y is written by one instruction.
-    constexpr int NCOL = NF * 32;          // output columns of a wave
     constexpr int RB = NCOL * 2;           // bytes of a staged row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int RPI = 64 / CPR;          // rows per store instruction
-    // chunk swizzle of a staged row: the 16 (or 8 pairs of) rows one write instruction
-    // touches spread over distinct bank groups
+    // chunk swizzle of a staged row: the 16 rows one write instruction touches spread over
+    // distinct bank groups
     auto row_swz = [](int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); };
     __builtin_amdgcn_s_waitcnt(kLgkm0);
     barrier_no_fence();
     char* stage = smem + wave * (128 * RB);
-    const int col0 = n0 + wn * NCOL;
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
+      const int c4 = f * 16 + 4 * q4;   // first of the lane's 4 columns in the wave block
+      float bgv[4], buv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      bias4<T, float>(p.bg, col0 + c4, p.N, true, bgv);
+      if constexpr (MODE == kGated) bias4<T, float>(p.bu, col0 + c4, p.N, true, buv);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int col = col0 + f * 32 + 8 * i + 4 * g;
-        float bgv[4], buv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        bias4<T, float>(p.bg, col, p.N, true, bgv);
-        if constexpr (MODE == kGated) bias4<T, float>(p.bu, col, p.N, true, buv);
+      for (int t = 0; t < 8; ++t) {
+        float v[4];
+        values(f, t, bgv, buv, v);
+        T o[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          float gv[4], uv[4], v[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            gv[j] = acc[f][t][4 * i + j];
-            uv[j] = MODE == kGated ? acc[f + 2][t][4 * i + j] : 0.0f;
-          }
-          finish4<T, MODE, ACT, float>(gv, uv, bgv, buv, v);
-          T o[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) o[j] = store_cast<T, float>(v[j]);
-          uint2 raw;
-          __builtin_memcpy(&raw, o, 8);
-          const int row = t * 32 + (lane & 31);
-          const int chunk = (4 * f + i) ^ row_swz(row);
-          *(uint2*)(stage + row * RB + chunk * 16 + g * 8) = raw;
-        }
+        for (int j = 0; j < 4; ++j) o[j] = store_cast<T, float>(v[j]);
+        uint2 raw;
+        __builtin_memcpy(&raw, o, 8);
+        const int row = t * 16 + (lane & 15);
+        const int chunk = (c4 >> 3) ^ row_swz(row);
+        *(uint2*)(stage + row * RB + chunk * 16 + (q4 & 1) * 8) = raw;
       }
     }
 #pragma unroll
@@ -385,27 +369,18 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
   }
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
+    const int col = col0 + f * 16 + 4 * q4;
+    if (col >= p.N) continue;
+    float bgv[4], buv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    bias4<T, float>(p.bg, col, p.N, vec, bgv);
+    if constexpr (MODE == kGated) bias4<T, float>(p.bu, col, p.N, vec, buv);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int col = MODE == kGated ? n0 + wn * 64 + f * 32 + 8 * i + 4 * g
-                                     : n0 + wn * 128 + f * 32 + 8 * i + 4 * g;
-      if (col >= p.N) continue;
-      float bgv[4], buv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      bias4<T, float>(p.bg, col, p.N, vec, bgv);
-      if constexpr (MODE == kGated) bias4<T, float>(p.bu, col, p.N, vec, buv);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int tok = tok0 + t * 32;
-        if (tok >= p.M) continue;
-        float gv[4], uv[4], v[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          gv[j] = acc[f][t][4 * i + j];
-          uv[j] = MODE == kGated ? acc[f + 2][t][4 * i + j] : 0.0f;
-        }
-        finish4<T, MODE, ACT, float>(gv, uv, bgv, buv, v);
-        store4<T, float>(y + (int64_t)tok * p.ldy, col, p.N, vec, v);
-      }
+    for (int t = 0; t < 8; ++t) {
+      const int tok = m0 + wm * 128 + t * 16 + (lane & 15);
+      if (tok >= p.M) continue;
+      float v[4];
+      values(f, t, bgv, buv, v);
+      store4<T, float>(y + (int64_t)tok * p.ldy, col, p.N, vec, v);
     }
   }
 }
