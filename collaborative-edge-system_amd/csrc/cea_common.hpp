@@ -144,7 +144,7 @@ __device__ __forceinline__ bool is_inf(double x) { return __builtin_isinf(x); }
 
 // Activations of the gated MLP (the reference's _ACTIVATIONS, llama.py:44-49), in f32 for
 // bf16 / f16 / f32 tensors and in f64 for f64, the way torch's elementwise kernels compute
-// them:
+// them (silu in f32 with the exp and quotient of exp_act / silu_f32 below, within a few ulp):
 //   silu              g / (1 + exp(-g))
 //   gelu              (g * 0.5) * (1 + erf(g * (1/sqrt 2)))
 //   gelu_pytorch_tanh (0.5 * g) * (1 + tanh(sqrt(2/pi) * (g + 0.044715 * g^3)))
@@ -156,8 +156,36 @@ template <typename M> __device__ __forceinline__ M tanh_acc(M x);
 template <> __device__ __forceinline__ float tanh_acc<float>(float x) { return tanhf(x); }
 template <> __device__ __forceinline__ double tanh_acc<double>(double x) { return tanh(x); }
 
+// e^x in f32 for the activations: 2^(x log2 e), with the rounding error of the product
+// x * log2(e) kept as an exact FMA remainder and applied as 2^t (1 + lo ln 2), so the result
+// stays within about 2 ulp for every x (v_exp_f32 is good to 1 ulp) instead of losing
+// accuracy as |x| grows.  x is clamped below at -104 (the result is 0 there either way), so
+// -inf gives 0; +inf gives NaN and finite x above 88.72 gives +inf.
+__device__ __forceinline__ float exp_act(float x) {
+  constexpr float kL2e = 1.44269502162933349609375f;   // log2(e) rounded to f32
+  constexpr float kL2eLo = 1.925963033500e-8f;          // log2(e) - kL2e
+  x = __builtin_fmaxf(x, -104.0f);
+  const float t = x * kL2e;
+  float lo = __builtin_fmaf(x, kL2e, -t);   // x * kL2e - t, exactly
+  lo = __builtin_fmaf(x, kL2eLo, lo);
+  const float p = __builtin_amdgcn_exp2f(t);
+  return __builtin_fmaf(p, lo * 0.693147180559945309417f, p);
+}
+
+// silu(g) = g / (1 + e^-g) in f32: the quotient from the reciprocal with one FMA correction
+// (the correctly rounded quotient but in rare cases), and g / inf = -0 as in IEEE division.
+__device__ __forceinline__ float silu_f32(float g) {
+  const float d = 1.0f + exp_act(-g);
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q = g * r;
+  const float q2 = __builtin_fmaf(__builtin_fmaf(-q, d, g), r, q);
+  return __builtin_isinf(d) ? q : q2;
+}
+
 template <int ACT, typename M> __device__ __forceinline__ M gate_act(M a) {
-  if constexpr (ACT == CEA_ACT_SILU) {
+  if constexpr (ACT == CEA_ACT_SILU && sizeof(M) == 4) {
+    return silu_f32(a);
+  } else if constexpr (ACT == CEA_ACT_SILU) {
     return div_rn(a, add_rn((M)1, exp_acc(-a)));
   } else if constexpr (ACT == CEA_ACT_GELU) {
     const M alpha = (M)0.70710678118654752440;  // 1/sqrt(2)

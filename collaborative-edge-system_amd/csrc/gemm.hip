@@ -16,14 +16,15 @@
 //     v_mfma_f32_16x16x32 (256 registers) live in the accumulation registers throughout;
 //   * the MFMA's A operand is the weight (16 rows) and B the tokens (16 columns), so the 4
 //     accumulator values of a lane are 4 consecutive output features of one token;
-//   * 32-wide K slices of both operands go global -> LDS directly (buffer_load ... lds)
-//     through a 4-buffer ring, 3 slices ahead of the one being multiplied; the 64-byte rows
-//     of a slice are XOR-swizzled in 16-byte groups so that the fragment reads
-//     (ds_read_b128) of any 8 or 16 consecutive lanes hit distinct banks;
-//   * one barrier per slice; the slice's 64 matrix instructions each carry a share of the
-//     rest: the 16 fragment reads of the next slice (one per 4) and the 8 loads that refill
-//     the buffer just freed (one per 8), so neither the LDS nor the address unit sees a burst
-//     that would hold every wave at once;
+//   * 64-wide K slices of both operands go global -> LDS directly (buffer_load ... lds) into
+//     two stages; a slice row is one 128-byte cache line, so each load instruction touches 8
+//     lines (the address unit's cost is per line touched); rows are XOR-swizzled in 16-byte
+//     groups so that the fragment reads (ds_read_b128) of any 8 or 16 consecutive lanes hit
+//     distinct banks;
+//   * one barrier per slice, between its two 32-wide steps; the 64 matrix instructions of a
+//     step each carry a share of the rest (the 16 fragment reads of the next step, one per 4,
+//     and in the second step the 16 loads that refill the buffer just freed, one per 4), so
+//     neither the LDS nor the address unit sees a burst that would hold every wave at once;
 //   * rows past M / N and columns past K read as zero through the buffer resources' range
 //     check, so ragged tiles take no branches in the loop;
 //   * the output block goes through LDS and leaves as whole 16-byte row chunks, so each
@@ -63,16 +64,16 @@ enum { kPlain = 0, kGated = 1 };
 constexpr int G_THREADS = 256;
 constexpr int G_BM = 256;                            // tokens per tile
 constexpr int G_BW = 256;                            // weight rows per tile
-constexpr int G_BK = 32;                             // K per LDS slice
-constexpr int G_ROW = G_BK * 2;                      // bytes of one row of a slice
-constexpr int G_NST = 4;                             // LDS ring depth
-constexpr int G_OPER = G_BM * G_ROW;                 // 16 KB per operand per slice
+constexpr int G_BK = 64;                             // K per LDS slice
+constexpr int G_ROW = G_BK * 2;                      // bytes of one row of a slice: a cache line
+constexpr int G_NST = 2;                             // LDS stages
+constexpr int G_OPER = G_BM * G_ROW;                 // 32 KB per operand per slice
 constexpr int G_STAGE = 2 * G_OPER;                  // weight slice, then token slice
 constexpr int G_LDS = G_NST * G_STAGE;               // 128 KB
 constexpr int G_LOADS = G_OPER / (G_THREADS * 16);   // 16-byte loads per lane per operand
 constexpr uint32_t kOutOfRange = 0x80000000u;        // above every resource's range
 constexpr int kLgkm0 = 0xC07F;   // s_waitcnt lgkmcnt(0), vmcnt / expcnt left at their maximum
-static_assert(G_LOADS == 4 && G_BM == G_BW, "the load pattern assumes 4 x 16 rows per wave");
+static_assert(G_LOADS == 8 && G_BM == G_BW, "the load pattern assumes 8 x 8 rows per wave");
 
 struct GemmParams {
   const void* x;    // [M, K], row stride ldx
@@ -87,14 +88,13 @@ struct GemmParams {
   int32_t vec_out;  // 2: 16-byte row chunks, 1: 4-element stores, 0: element stores
 };
 
-// 16-byte group swizzle of a slice row (4 groups of 16 bytes): group c of row r sits at group
-// c ^ g_swz(r).  Among any 16 consecutive rows the 4 rows of equal r & 3 get distinct values,
-// and among any 8 consecutive rows the 4 of equal parity do, so the 16-lane groups of a
-// fragment read (16 rows, one group) hit distinct 16-byte bank groups within 256 bytes and
-// 8-lane groups within 128 bytes.  Depends on r & 15 only.
-__device__ __forceinline__ int g_swz(int r) {
-  return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) << 1);
-}
+// 16-byte group swizzle of a slice row (8 groups of 16 bytes): group c of row r sits at group
+// c ^ g_swz(r).  A fragment read has 16 rows per 16-lane quarter and the quarters read groups
+// c, c+1, c+2, c+3.  Measured on gfx950 (LDS bank-conflict counter), the reads behave as if 32
+// lanes share a 512-byte bank window; this swizzle gives distinct 16-byte slots for any 32
+// lanes (rows of equal r & 3 in one window), for any 16 lanes within 256 bytes and for any 8
+// within 128 bytes.  Depends on r & 15 only.
+__device__ __forceinline__ int g_swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
 // Tile (token block, weight block) of this workgroup.
 __device__ __forceinline__ void tile_of(const GemmParams& p, int& tm, int& tn) {
@@ -158,16 +158,16 @@ __device__ __forceinline__ void store4(T* row, int col, int n, bool vec, const A
 
 // The epilogue of 4 consecutive columns: plain y = acc + bias; gated
 // y = T(act(T(gate + b_g))) * T(up + b_u).
-template <typename T, int MODE, int ACT, typename A>
+template <typename T, int MODE, int ACT, bool BIAS, typename A>
 __device__ __forceinline__ void finish4(const A (&g)[4], const A (&u)[4], const A (&bg)[4],
                                         const A (&bu)[4], A (&v)[4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if constexpr (MODE == kPlain) {
-      v[j] = add_rn(g[j], bg[j]);
+      v[j] = BIAS ? add_rn(g[j], bg[j]) : g[j];
     } else {
-      const A gate = rnd_acc<T, A>(add_rn(g[j], bg[j]));
-      const A up = rnd_acc<T, A>(add_rn(u[j], bu[j]));
+      const A gate = rnd_acc<T, A>(BIAS ? add_rn(g[j], bg[j]) : g[j]);
+      const A up = rnd_acc<T, A>(BIAS ? add_rn(u[j], bu[j]) : u[j]);
       v[j] = mul_rn(rnd_acc<T, A>(gate_act<ACT, A>(gate)), up);
     }
   }
@@ -208,17 +208,19 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
                    (uint32_t)((int64_t)(rows - 1) * p.ldw * ESZ + (int64_t)K * ESZ));
   }
 
-  // Slice loads: wave w fills rows [64w, 64w + 64) of both operands, 16 rows x 64 bytes per
-  // instruction; lane l brings 16-byte group (l & 3) ^ g_swz(row) of row 64w + 16i + (l >> 2)
-  // to group l & 3 (g_swz(row) only depends on row & 15 = l >> 2).  The per-lane offsets
-  // stay fixed; the slice's K offset is the scalar soffset, and groups past K (the last
-  // slice of a K that is not a multiple of 32) get an offset past the resource's range.
-  const int grp = (lane & 3) ^ g_swz(lane >> 2);
-  const int kcol = grp * 8;   // first element column of the lane's group in a slice
+  // Slice loads: wave w fills rows [64w, 64w + 64) of both operands, 8 rows x 128 bytes (one
+  // cache line each) per instruction; lane l brings 16-byte group (l & 7) ^ g_swz(row) of row
+  // 64w + 8i + (l >> 3) to group l & 7 (row & 15 = 8 (i & 1) + (l >> 3)).  The per-lane
+  // offsets stay fixed; the slice's K offset is the scalar soffset, and groups past K (the
+  // last slice of a K that is not a multiple of 64, and the slices past it) get an offset past
+  // the resource's range, i.e. load zeros.
+  int kcol[2];   // first element column of the lane's group in a slice, for even / odd i
   uint32_t off_w[G_LOADS], off_x[G_LOADS];
 #pragma unroll
   for (int i = 0; i < G_LOADS; ++i) {
-    const int row = 64 * wave + 16 * i + (lane >> 2);
+    const int row = 64 * wave + 8 * i + (lane >> 3);
+    const int grp = (lane & 7) ^ g_swz(row);
+    if (i < 2) kcol[i] = grp * 8;
     const int wrow = MODE == kGated ? (row & 127) : row;
     off_w[i] = (uint32_t)((int64_t)wrow * p.ldw * ESZ) + grp * 16;
     off_x[i] = (uint32_t)((int64_t)row * p.ldx * ESZ) + grp * 16;
@@ -228,26 +230,29 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
   auto issue_one = [&](int s, int i) {
     const uint32_t sb = lds_wave + (uint32_t)(s & (G_NST - 1)) * G_STAGE;
     const uint32_t kb = (uint32_t)s * G_ROW;
-    const bool kin = s * G_BK + kcol < K;
+    const int li = i < G_LOADS ? i : i - G_LOADS;
+    const bool kin = s * G_BK + kcol[li & 1] < K;
     if (i < G_LOADS)
-      buffer_load_lds16_m0_so(rw, sb + i * 1024, kin ? off_w[i] : kOutOfRange, kb);
+      buffer_load_lds16_m0_so(rw, sb + li * 1024, kin ? off_w[li] : kOutOfRange, kb);
     else
-      buffer_load_lds16_m0_so(rx, sb + G_OPER + (i - G_LOADS) * 1024,
-                              kin ? off_x[i - G_LOADS] : kOutOfRange, kb);
+      buffer_load_lds16_m0_so(rx, sb + G_OPER + li * 1024, kin ? off_x[li] : kOutOfRange, kb);
   };
 
   // Fragment reads (v_mfma_f32_16x16x32): lane l takes row (l & 15) of a 16-row block and
-  // its 8 elements of group l >> 4; blocks start at multiples of 16 rows, so the swizzled
-  // position only depends on the lane.  Fragment j < 8 is weight block j, j >= 8 token
-  // block j - 8.
-  const uint32_t rd = (lane & 15) * G_ROW + ((((lane >> 4)) ^ g_swz(lane & 15)) << 4);
+  // its 8 elements of group 4q + (l >> 4) for the 32-wide step q of the slice; blocks start
+  // at multiples of 16 rows, so the swizzled position only depends on the lane.  Fragment
+  // j < 8 is weight block j, j >= 8 token block j - 8.
+  uint32_t rd[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    rd[q] = (lane & 15) * G_ROW + (((4 * q + (lane >> 4)) ^ g_swz(lane & 15)) << 4);
   auto frag_row = [&](int j) {   // first LDS row of fragment j inside a stage
     if (j < 8)
       return MODE == kGated ? (j >> 2) * 128 + wn * 64 + (j & 3) * 16 : wn * 128 + j * 16;
     return G_BM + wm * 128 + (j - 8) * 16;   // token rows follow the 256 weight rows
   };
-  auto read_one = [&](int s, int j, frag (&fa)[8], frag (&fb)[8]) {
-    const char* a = smem + (s & (G_NST - 1)) * G_STAGE + rd + frag_row(j) * G_ROW;
+  auto read_one = [&](int s, int q, int j, frag (&fa)[8], frag (&fb)[8]) {
+    const char* a = smem + (s & (G_NST - 1)) * G_STAGE + rd[q] + frag_row(j) * G_ROW;
     if (j < 8) fa[j] = *(const frag*)a;
     else fb[j - 8] = *(const frag*)a;
   };
@@ -260,49 +265,48 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[f][t][e] = 0.0f;
 
-  // The 64 matrix instructions of slice s (fragments fa / fb), each followed by a share of
-  // the other work: the 16 fragment reads of slice s + 1 (one per 4 instructions, into
-  // na / nb) and the 8 loads of slice s + 4 into the buffer slice s leaves (one per 8), so
-  // neither the LDS nor the address unit ever sees a burst.
-  auto slice = [&](int s, const frag (&fa)[8], const frag (&fb)[8], frag (&na)[8], frag (&nb)[8]) {
+  // The 64 matrix instructions of step q of slice s (fragments fa / fb), each followed by a
+  // share of the other work: the 16 fragment reads of the next step (slice rs, step rq; one
+  // per 4 instructions, into na / nb) and, with DMA, the 16 loads of slice s + 2 into the
+  // buffer slice s leaves (one per 4), so neither the LDS nor the address unit sees a burst.
+  auto step = [&](int s, const frag (&fa)[8], const frag (&fb)[8], int rs, int rq, frag (&na)[8],
+                  frag (&nb)[8], auto dma) {
 #pragma unroll
     for (int f = 0; f < 8; ++f)
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const int i = f * 8 + t;
         acc[f][t] = GMfma<T>::run(fa[f], fb[t], acc[f][t]);
-        if ((i & 3) == 0) read_one(s + 1, i >> 2, na, nb);
-        if ((i & 7) == 4) issue_one(s + G_NST, i >> 3);
+        if ((i & 3) == 0) read_one(rs, rq, i >> 2, na, nb);
+        if constexpr (decltype(dma)::value) {
+          if ((i & 3) == 2) issue_one(s + G_NST, i >> 2);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
   };
-  // The barrier before slice s: slice s + 1 has landed for every wave (this wave issued
-  // slices s + 2 and s + 3 after it), and every wave has read all of slice s, whose buffer
-  // slice s refills.
-  auto sync = [&]() {
-    wait_vmcnt<2 * 2 * G_LOADS>();
-    __builtin_amdgcn_s_waitcnt(kLgkm0);
-    barrier_no_fence();
-    __builtin_amdgcn_sched_barrier(0);
-  };
 
-  // Slices at or past KT are loaded with every offset out of range, i.e. as zeros: the loop
-  // runs uniformly (always 3 slices ahead, always reading the next slice), and the extra slice
-  // that rounds KT up to an even count adds exact zeros.
+  // Two stages.  Per slice s: step 0 reads the fragments of step 1; then one barrier (slice
+  // s + 1 has landed, every wave has read all of slice s); step 1 reads the first fragments
+  // of slice s + 1 and refills the buffer of slice s with slice s + 2, which then has a whole
+  // step before it is needed.  Slices at or past KT load as zeros, so the loop runs
+  // uniformly and its last refills and reads are harmless.
   frag fa0[8], fb0[8], fa1[8], fb1[8];
 #pragma unroll
   for (int s = 0; s < G_NST; ++s)
 #pragma unroll
     for (int i = 0; i < 2 * G_LOADS; ++i) issue_one(s, i);
-  wait_vmcnt<3 * 2 * G_LOADS>();
+  wait_vmcnt<2 * G_LOADS>();
   barrier_no_fence();
 #pragma unroll
-  for (int j = 0; j < 16; ++j) read_one(0, j, fa0, fb0);
-  for (int s = 0; s < KT; s += 2) {   // two slices per trip: the fragment sets alternate
-    sync();
-    slice(s, fa0, fb0, fa1, fb1);
-    sync();
-    slice(s + 1, fa1, fb1, fa0, fb0);
+  for (int j = 0; j < 16; ++j) read_one(0, 0, j, fa0, fb0);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int s = 0; s < KT; ++s) {
+    step(s, fa0, fb0, s, 1, fa1, fb1, std::integral_constant<bool, false>());
+    wait_vmcnt<0>();                     // slice s + 1 is in
+    __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's reads of slice s are done
+    barrier_no_fence();
+    __builtin_amdgcn_sched_barrier(0);
+    step(s, fa1, fb1, s + 1, 0, fa0, fb0, std::integral_constant<bool, true>());
   }
   wait_vmcnt<0>();   // the last refills (zeros) land before the LDS is used again
 
@@ -314,14 +318,15 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
   constexpr int NF = MODE == kGated ? 4 : 8;   // output column blocks of 16 per wave
   constexpr int NCOL = NF * 16;                // output columns of a wave
   const int col0 = n0 + wn * NCOL;
-  auto values = [&](int f, int t, const float (&bgv)[4], const float (&buv)[4], float (&v)[4]) {
+  auto values = [&](int f, int t, const float (&bgv)[4], const float (&buv)[4], float (&v)[4],
+                    auto bias) {
     float gv[4], uv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       gv[j] = acc[f][t][j];
       uv[j] = MODE == kGated ? acc[f + 4][t][j] : 0.0f;
     }
-    finish4<T, MODE, ACT, float>(gv, uv, bgv, buv, v);
+    finish4<T, MODE, ACT, decltype(bias)::value, float>(gv, uv, bgv, buv, v);
   };
   if (p.vec_out == 2) {
     // Staged through LDS (free once every wave has read its last fragments): each wave
@@ -336,26 +341,32 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
     __builtin_amdgcn_s_waitcnt(kLgkm0);
     barrier_no_fence();
     char* stage = smem + wave * (128 * RB);
+    auto to_lds = [&](auto bias) {
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      const int c4 = f * 16 + 4 * q4;   // first of the lane's 4 columns in the wave block
-      float bgv[4], buv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      bias4<T, float>(p.bg, col0 + c4, p.N, true, bgv);
-      if constexpr (MODE == kGated) bias4<T, float>(p.bu, col0 + c4, p.N, true, buv);
+      for (int f = 0; f < NF; ++f) {
+        const int c4 = f * 16 + 4 * q4;   // first of the lane's 4 columns in the wave block
+        float bgv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, buv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (decltype(bias)::value) {
+          bias4<T, float>(p.bg, col0 + c4, p.N, true, bgv);
+          if constexpr (MODE == kGated) bias4<T, float>(p.bu, col0 + c4, p.N, true, buv);
+        }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        float v[4];
-        values(f, t, bgv, buv, v);
-        T o[4];
+        for (int t = 0; t < 8; ++t) {
+          float v[4];
+          values(f, t, bgv, buv, v, bias);
+          T o[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = store_cast<T, float>(v[j]);
-        uint2 raw;
-        __builtin_memcpy(&raw, o, 8);
-        const int row = t * 16 + (lane & 15);
-        const int chunk = (c4 >> 3) ^ row_swz(row);
-        *(uint2*)(stage + row * RB + chunk * 16 + (q4 & 1) * 8) = raw;
+          for (int j = 0; j < 4; ++j) o[j] = store_cast<T, float>(v[j]);
+          uint2 raw;
+          __builtin_memcpy(&raw, o, 8);
+          const int row = t * 16 + (lane & 15);
+          const int chunk = (c4 >> 3) ^ row_swz(row);
+          *(uint2*)(stage + row * RB + chunk * 16 + (q4 & 1) * 8) = raw;
+        }
       }
-    }
+    };
+    if (p.bg != nullptr) to_lds(std::integral_constant<bool, true>());
+    else to_lds(std::integral_constant<bool, false>());
 #pragma unroll
     for (int k = 0; k < 128 / RPI; ++k) {
       const int row = k * RPI + lane / CPR;
@@ -379,7 +390,7 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
       const int tok = m0 + wm * 128 + t * 16 + (lane & 15);
       if (tok >= p.M) continue;
       float v[4];
-      values(f, t, bgv, buv, v);
+      values(f, t, bgv, buv, v, std::integral_constant<bool, true>());
       store4<T, float>(y + (int64_t)tok * p.ldy, col, p.N, vec, v);
     }
   }
@@ -467,7 +478,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const GemmParams p) {
       gv[j] = acc[0][i][j];
       uv[j] = MODE == kGated ? acc[NW - 1][i][j] : A(0);
     }
-    finish4<T, MODE, ACT, A>(gv, uv, bgv, buv, v);
+    finish4<T, MODE, ACT, true, A>(gv, uv, bgv, buv, v);
     store4<T, A>(y + (int64_t)tok * p.ldy, col, p.N, false, v);
   }
 }
