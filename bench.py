@@ -7,7 +7,8 @@ each block merged exactly into the running (out, lse) in the kernel epilogue, ou
 bf16 (``ring_attention``).  Value = algorithmic TFLOP/s over visible (query, key) pairs.
 
 The same JSON line also reports the other workloads of the path (distributed-KV decode +
-merge, RMSNorm+rotary and SiLU-gate, the Ulysses share, the f32 split-merge check), the
+merge, RMSNorm+rotary and SiLU-gate, the Ulysses share, the f32 split-merge check, the fused
+gate/up and Q/K/V projections), the
 roofline of the dominant kernel measured live with HIP events on the launch stream, and the
 CPU oracle timed on a bounded sample of the headline workload on this host.
 
@@ -293,6 +294,53 @@ def bench_f32_split(cea, torch, steps, warmup, dev):
             "workload": "f32 attention B=1 8/8 heads S=512 D=64 causal, 2-way KV split + merge"}
 
 
+def _paired_timed(fn_a, fn_b, steps: int, warmup: int, torch, dev, rounds: int = 3):
+    """Alternating timings of two routes to the same result (``rounds`` x ``steps`` calls each,
+    wall clock around host synchronisation, plus HIP events on the launch stream), so both
+    see the same clock and power state; returns the best round of each as (wall s, GPU ms)."""
+    best = {}
+    for _ in range(rounds):
+        for key, fn in (("a", fn_a), ("b", fn_b)):
+            sec, gpu_ms = _event_timed(fn, steps, warmup, torch, dev)
+            if key not in best or sec < best[key][0]:
+                best[key] = (sec, gpu_ms)
+    return best["a"], best["b"]
+
+
+def bench_projection(cea, torch, steps, warmup, dev):
+    """The fused projections on this package's gfx950 GEMM: gate/up with the SiLU gate in the
+    epilogue (one kernel, no [M, 2I] intermediate) against PyTorch's own route to the same
+    result (library GEMM + this package's gate kernel), and the Q/K/V projection against
+    PyTorch's library GEMM; each pair timed alternately."""
+    w = cea.workloads.projections(device=dev)
+    n = w.inter
+    wg, wu = w.w_gate_up[:n], w.w_gate_up[n:]
+    F = torch.nn.functional
+    res = {}
+    (sec, gpu_ms), (ref_sec, _) = _paired_timed(
+        lambda: cea.linear_gated(w.x_mlp, wg, wu, act="silu"),
+        lambda: cea.gated_mul(*F.linear(w.x_mlp, w.w_gate_up).split([n, n], -1), "silu"),
+        steps, warmup, torch, dev)
+    tf = w.flop_gate_up / sec / 1e12
+    res["gate_up_silu"] = {"value": round(tf, 1), "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                           "us_per_step": round(sec * 1e6, 1), "gpu_us_per_step": round(gpu_ms * 1e3, 1),
+                           "flop": w.flop_gate_up,
+                           "torch_route_us": round(ref_sec * 1e6, 1),
+                           "speedup_vs_torch_route": round(ref_sec / sec, 3)}
+    (sec, gpu_ms), (ref_sec, _) = _paired_timed(lambda: cea.linear(w.x_attn, w.w_qkv),
+                                                lambda: F.linear(w.x_attn, w.w_qkv),
+                                                steps, warmup, torch, dev)
+    tf = w.flop_qkv / sec / 1e12
+    res["qkv"] = {"value": round(tf, 1), "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                  "us_per_step": round(sec * 1e6, 1), "gpu_us_per_step": round(gpu_ms * 1e3, 1),
+                  "flop": w.flop_qkv, "torch_route_us": round(ref_sec * 1e6, 1),
+                  "speedup_vs_torch_route": round(ref_sec / sec, 3)}
+    res["workload"] = ("Llama-3-8B-shaped fused projections, bf16: gate/up 4096 tokens x 4096 -> "
+                       "2 x 14336 with SiLU fused (torch route: F.linear + gate kernel); Q/K/V 8192 "
+                       "tokens x 4096 -> 6144 (torch route: F.linear); best of 3 alternating rounds")
+    return res
+
+
 def _median_time(fn, reps: int) -> float:
     fn()  # one warm-up
     times = []
@@ -330,7 +378,8 @@ def cpu_baseline(cea, torch):
     and layer-op sequence) on the five workloads, timed on this host's cores with
     ``time.perf_counter``: one warm-up, then the median of N repetitions (N = 5 for the f32
     split-merge, the layer ops and the decode sample; 1 for the ring share, which runs in
-    full; the Ulysses share on a stated subset of query rows).  Rates use the same
+    full; the Ulysses share on a stated subset of query rows; 3 for the projections, on 1024
+    tokens of each).  Rates use the same
     algorithmic FLOP / byte counts as the GPU lines.  The top-level fields are the headline
     ring share's."""
     from oracle import attention_ref as ref
@@ -414,6 +463,23 @@ def cpu_baseline(cea, torch):
                                           "spaced chunks of 64) x 65536 keys"}
     del w5
 
+    # fused projections: 1024 of the 4096 gate/up tokens (the oracle's F.linear on the CPU in
+    # bf16, then act(gate) * up) and 1024 of the 8192 Q/K/V tokens
+    w6 = cea.workloads.projections(device="cpu")
+    xs, xa = w6.x_mlp[:1024], w6.x_attn[:1024]
+    n6 = w6.inter
+    t = _median_time(lambda: lref.gated(lref.linear(xs, w6.w_gate_up[:n6]),
+                                        lref.linear(xs, w6.w_gate_up[n6:]), "silu"), 3)
+    proj = {"gate_up_silu": {"value": round(w6.flop_gate_up * 1024 / w6.x_mlp.shape[0] / t / 1e12, 4),
+                             "unit": "TFLOP/s", "ms_per_step": round(t * 1e3, 2)}}
+    t = _median_time(lambda: lref.linear(xa, w6.w_qkv), 3)
+    proj["qkv"] = {"value": round(w6.flop_qkv * 1024 / w6.x_attn.shape[0] / t / 1e12, 4),
+                   "unit": "TFLOP/s", "ms_per_step": round(t * 1e3, 2)}
+    proj["reps"] = 3
+    proj["sample"] = "1024 tokens of each projection, full weights"
+    configs["projection"] = proj
+    del w6
+
     return {"value": ring["value"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": ring["sample"] + "; the other workloads under 'configs'",
             "host": _host_info(threads), "configs": configs}
@@ -449,7 +515,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of: ring,decode,layers,kvappend,ulysses,wire,f32")
+    ap.add_argument("--only", default="",
+                    help="comma list of: ring,decode,layers,kvappend,ulysses,wire,f32,proj")
     ap.add_argument("--trace-summary", default="", metavar="CSV",
                     help="only summarise a rocprofv3 kernel-trace CSV (the last --last "
                          "dispatches of every kernel) and exit")
@@ -503,6 +570,9 @@ def main() -> int:
         secondary["wire"] = bench_wire(cea, torch, args.steps, args.warmup, dev)
     if want("f32"):
         secondary["attn_f32_split"] = bench_f32_split(cea, torch, args.steps, args.warmup, dev)
+    if want("proj"):
+        _log("fused projections (gate/up + SiLU, Q/K/V)")
+        secondary["projection"] = bench_projection(cea, torch, 10, max(5, args.warmup), dev)
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline (oracle)")

@@ -17,6 +17,8 @@ CPU oracle and the GPU see bit-identical inputs.
   uniform in [1024, 32768]; four contiguous partitions with weights 0.4/0.3/0.2/0.1.
 * ``ulysses_share``    - rank 0 of an 8-way Ulysses split of a 64/16-head model: 65536 tokens,
   8/2 heads, D=128, bf16, causal, 4 packed sequences followed by right padding.
+* ``projections``      - the fused gate/up (4096 tokens, 4096 -> 2 x 14336, SiLU) and Q/K/V
+  (8192 tokens, 4096 -> 32/8/8 heads x 128) projections of a Llama-3-8B-shaped layer, bf16.
 * ``kv_append``        - one rank's 8192-token prefill chunk (8 KV heads, D=128, bf16, theta
   1e4) rotated and appended into a head-major cache that already holds 8192 tokens.
 """
@@ -104,6 +106,39 @@ def layer_ops(device="cpu", seed: int = 0, tokens: int = 4096, hidden: int = 409
     up = _randn(g, tokens, inter, device=device)
     pos = torch.arange(tokens, device=device).view(1, tokens)
     return LayerOps(x, w, pos, gate, up)
+
+
+# --------------------------------------------------------------------------------------
+@dataclass
+class Projections:
+    """The fused projections of a Llama-3-8B-shaped layer (hidden 4096, 32/8 heads x 128,
+    intermediate 14336) on one device: the gate/up projection of 4096 tokens with SiLU, and
+    the Q/K/V projection of the ring share's 8192 local tokens."""
+    x_mlp: torch.Tensor      # [4096, 4096]
+    w_gate_up: torch.Tensor  # [2 * 14336, 4096], gate rows first
+    x_attn: torch.Tensor     # [8192, 4096]
+    w_qkv: torch.Tensor      # [(32 + 8 + 8) * 128, 4096]
+    inter: int = 14336
+
+    @property
+    def flop_gate_up(self) -> int:
+        return 2 * self.x_mlp.shape[0] * self.x_mlp.shape[1] * self.w_gate_up.shape[0]
+
+    @property
+    def flop_qkv(self) -> int:
+        return 2 * self.x_attn.shape[0] * self.x_attn.shape[1] * self.w_qkv.shape[0]
+
+
+def projections(device="cpu", seed: int = 0, mlp_tokens: int = 4096, attn_tokens: int = 8192,
+                hidden: int = 4096, inter: int = 14336, hq: int = 32, hkv: int = 8,
+                d: int = 128) -> Projections:
+    g = _gen(seed)
+    scale = hidden ** -0.5
+    x_mlp = _randn(g, mlp_tokens, hidden, device=device)
+    w_gu = (torch.randn(2 * inter, hidden, generator=g) * scale).to(torch.bfloat16).to(device)
+    x_attn = _randn(g, attn_tokens, hidden, device=device)
+    w_qkv = (torch.randn((hq + 2 * hkv) * d, hidden, generator=g) * scale).to(torch.bfloat16).to(device)
+    return Projections(x_mlp, w_gu, x_attn, w_qkv, inter)
 
 
 # --------------------------------------------------------------------------------------
