@@ -336,3 +336,46 @@ def test_oracle_linear_closed_form(bias):
     assert not close(L.linear(x, w.T.contiguous(), b))
     if bias:
         assert not close(L.linear(x, w, None))
+
+
+# ---------------------------------------------------------------------------------------
+# linear (tensor_parallel.py:294-295): F.linear in the input dtype on the CPU
+# ---------------------------------------------------------------------------------------
+def _exact_linear(x, w, b):
+    y = x.double() @ w.double().t()
+    return y if b is None else y + b.double()
+
+
+def test_linear_f64_closed_form():
+    """y[i, j] = sum_k x[i, k] w[j, k] + b[j]: integer-valued operands make every product and
+    sum exact, so the oracle must return the exact integers (a transposed weight, a dropped
+    bias or a wrong contraction axis changes them)."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randint(-8, 9, (5, 7), generator=g).double()
+    w = torch.randint(-8, 9, (3, 7), generator=g).double()
+    b = torch.randint(-8, 9, (3,), generator=g).double()
+    want = torch.tensor([[sum(x[i, k].item() * w[j, k].item() for k in range(7)) + b[j].item()
+                          for j in range(3)] for i in range(5)], dtype=torch.float64)
+    assert torch.equal(L.linear(x, w, b), want)
+    assert torch.equal(L.linear(x, w), want - b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_linear_reduced_precision_rounds_once(dtype):
+    """bf16 / f16 F.linear accumulates in f32 and rounds once: within the f32 accumulation
+    bound of the exact result, and equal to the correctly rounded exact value for almost
+    every element (a per-term rounding to the dtype would break both)."""
+    g = torch.Generator().manual_seed(5)
+    m, k, n = 64, 1024, 96
+    x = torch.randn(m, k, generator=g).to(dtype)
+    w = (torch.randn(n, k, generator=g) / 32).to(dtype)
+    b = torch.randn(n, generator=g).to(dtype)
+    y = L.linear(x, w, b)
+    exact = _exact_linear(x, w, b)
+    mags = x.double().abs() @ w.double().abs().t() + b.double().abs()
+    gam = (k + 2) * 2.0 ** -24 * mags
+    mant = 7 if dtype == torch.bfloat16 else 10
+    e = torch.floor(torch.log2((exact.abs() + gam).clamp(min=2.0 ** -30)))
+    ulp = torch.pow(2.0, e - mant)
+    assert bool(((y.double() - exact).abs() <= ulp / 2 + gam).all())
+    assert (y == exact.to(dtype)).double().mean().item() >= 0.99
