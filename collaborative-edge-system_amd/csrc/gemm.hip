@@ -11,22 +11,26 @@
 //          [M, 2I] gate/up intermediate never reaches memory.
 //
 // Matrix-core kernel (bf16 / f16, 16-byte aligned rows, K a multiple of 8):
-//   * one workgroup = 4 waves, one per SIMD (512 registers each), computes 256 tokens x 256
-//     weight rows; each wave owns a 128 x 128 block whose 64 accumulators of
-//     v_mfma_f32_16x16x32 (256 registers) live in the accumulation registers throughout;
+//   * one workgroup = 8 waves, two per SIMD (256 registers each), computes 256 tokens x 256
+//     weight rows; each wave owns 128 tokens x 64 weight rows, 32 accumulators of
+//     v_mfma_f32_16x16x32 (128 registers); with two waves per SIMD one wave's stalls (load
+//     issue, barrier, the activation epilogue's transcendental latencies) leave the matrix
+//     core to the other;
 //   * the MFMA's A operand is the weight (16 rows) and B the tokens (16 columns), so the 4
 //     accumulator values of a lane are 4 consecutive output features of one token;
 //   * 64-wide K slices of both operands go global -> LDS directly (buffer_load ... lds) into
 //     two stages; a slice row is one 128-byte cache line, so each load instruction touches 8
 //     lines (the address unit's cost is per line touched); rows are XOR-swizzled in 16-byte
-//     groups so that the fragment reads (ds_read_b128) of any 8 or 16 consecutive lanes hit
-//     distinct banks;
-//   * one barrier per slice, between its two 32-wide steps; the 64 matrix instructions of a
-//     step each carry a share of the rest (the 16 fragment reads of the next step, one per 4,
-//     and in the second step the 16 loads that refill the buffer just freed, one per 4), so
-//     neither the LDS nor the address unit sees a burst that would hold every wave at once;
+//     groups so that the fragment reads (ds_read_b128) hit distinct banks;
+//   * one barrier per slice, between its two 32-wide steps; a step's 32 matrix instructions
+//     run token-block major and each carries a share of the rest: every token fragment is
+//     reloaded for the next step right after its last use (so only one token set is held),
+//     the next weight fragments go into a second set, and in the second step the 8 loads
+//     refilling the buffer just freed go out one per 4 instructions, so neither the LDS nor
+//     the address unit sees a burst;
 //   * rows past M / N and columns past K read as zero through the buffer resources' range
-//     check, so ragged tiles take no branches in the loop;
+//     check, so ragged tiles take no branches in the loop; slices past K load as zeros, so the
+//     loop runs uniformly;
 //   * the output block goes through LDS and leaves as whole 16-byte row chunks, so each
 //     cache line of y is written by one store instruction;
 //   * workgroups are dealt to the 8 XCDs round robin; tiles are renumbered so that each XCD
@@ -61,7 +65,7 @@ template <> struct GMfma<f16> {
 
 enum { kPlain = 0, kGated = 1 };
 
-constexpr int G_THREADS = 256;
+constexpr int G_THREADS = 512;                       // 8 waves, two per SIMD
 constexpr int G_BM = 256;                            // tokens per tile
 constexpr int G_BW = 256;                            // weight rows per tile
 constexpr int G_BK = 64;                             // K per LDS slice
@@ -73,7 +77,7 @@ constexpr int G_LDS = G_NST * G_STAGE;               // 128 KB
 constexpr int G_LOADS = G_OPER / (G_THREADS * 16);   // 16-byte loads per lane per operand
 constexpr uint32_t kOutOfRange = 0x80000000u;        // above every resource's range
 constexpr int kLgkm0 = 0xC07F;   // s_waitcnt lgkmcnt(0), vmcnt / expcnt left at their maximum
-static_assert(G_LOADS == 8 && G_BM == G_BW, "the load pattern assumes 8 x 8 rows per wave");
+static_assert(G_LOADS == 4 && G_BM == G_BW, "the load pattern assumes 4 x 8 rows per wave");
 
 struct GemmParams {
   const void* x;    // [M, K], row stride ldx
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int wm = wave & 1;    // token half of the tile
-  const int wn = wave >> 1;   // weight half (gated: output-column half)
+  const int wn = wave >> 1;   // weight quarter (gated: output-column quarter)
   int tm, tn;
   tile_of(p, tm, tn);
   const int m0 = tm * G_BM;
@@ -192,15 +196,13 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
   const int K = p.K;
   const int KT = (K + G_BK - 1) / G_BK;
 
-  // buffer resources: the tile's token rows; the weight rows this wave loads (gated: waves
-  // 0-1 load the 128 gate rows, waves 2-3 the matching 128 up rows)
   const int rows_x = min(G_BM, p.M - m0);
   const i32x4 rx = make_rsrc((const char*)p.x + (int64_t)m0 * p.ldx * ESZ,
                              (uint32_t)((int64_t)(rows_x - 1) * p.ldx * ESZ + (int64_t)K * ESZ));
   i32x4 rw;
-  if constexpr (MODE == kGated) {
+  if constexpr (MODE == kGated) {   // waves 0-3 load the 128 gate rows, 4-7 the 128 up rows
     const int rows = min(OUT_N, p.N - n0);
-    const char* base = (const char*)(wave < 2 ? p.wg : p.wu) + (int64_t)n0 * p.ldw * ESZ;
+    const char* base = (const char*)(wave < 4 ? p.wg : p.wu) + (int64_t)n0 * p.ldw * ESZ;
     rw = make_rsrc(base, (uint32_t)((int64_t)(rows - 1) * p.ldw * ESZ + (int64_t)K * ESZ));
   } else {
     const int rows = min(G_BW, p.N - n0);
@@ -208,17 +210,13 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
                    (uint32_t)((int64_t)(rows - 1) * p.ldw * ESZ + (int64_t)K * ESZ));
   }
 
-  // Slice loads: wave w fills rows [64w, 64w + 64) of both operands, 8 rows x 128 bytes (one
-  // cache line each) per instruction; lane l brings 16-byte group (l & 7) ^ g_swz(row) of row
-  // 64w + 8i + (l >> 3) to group l & 7 (row & 15 = 8 (i & 1) + (l >> 3)).  The per-lane
-  // offsets stay fixed; the slice's K offset is the scalar soffset, and groups past K (the
-  // last slice of a K that is not a multiple of 64, and the slices past it) get an offset past
-  // the resource's range, i.e. load zeros.
-  int kcol[2];   // first element column of the lane's group in a slice, for even / odd i
+  // slice loads: wave w fills rows [32w, 32w + 32) of both operands, 8 rows x 128 bytes per
+  // instruction (same lane pattern and swizzle as the 4-wave kernel)
+  int kcol[2];
   uint32_t off_w[G_LOADS], off_x[G_LOADS];
 #pragma unroll
   for (int i = 0; i < G_LOADS; ++i) {
-    const int row = 64 * wave + 8 * i + (lane >> 3);
+    const int row = 32 * wave + 8 * i + (lane >> 3);
     const int grp = (lane & 7) ^ g_swz(row);
     if (i < 2) kcol[i] = grp * 8;
     const int wrow = MODE == kGated ? (row & 127) : row;
@@ -226,8 +224,7 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
     off_x[i] = (uint32_t)((int64_t)row * p.ldx * ESZ) + grp * 16;
   }
   const uint32_t lds_wave = lds_addr(smem) + wave * G_LOADS * 1024;
-  // load i of slice s (i < G_LOADS: weight rows, else token rows)
-  auto issue_one = [&](int s, int i) {
+  auto issue_one = [&](int s, int i) {   // i < G_LOADS: weight rows, else token rows
     const uint32_t sb = lds_wave + (uint32_t)(s & (G_NST - 1)) * G_STAGE;
     const uint32_t kb = (uint32_t)s * G_ROW;
     const int li = i < G_LOADS ? i : i - G_LOADS;
@@ -238,46 +235,45 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
       buffer_load_lds16_m0_so(rx, sb + G_OPER + li * 1024, kin ? off_x[li] : kOutOfRange, kb);
   };
 
-  // Fragment reads (v_mfma_f32_16x16x32): lane l takes row (l & 15) of a 16-row block and
-  // its 8 elements of group 4q + (l >> 4) for the 32-wide step q of the slice; blocks start
-  // at multiples of 16 rows, so the swizzled position only depends on the lane.  Fragment
-  // j < 8 is weight block j, j >= 8 token block j - 8.
+  // fragments: 4 weight blocks (j < 4) and 8 token blocks (j >= 4) of 16 rows per step
   uint32_t rd[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q)
     rd[q] = (lane & 15) * G_ROW + (((4 * q + (lane >> 4)) ^ g_swz(lane & 15)) << 4);
-  auto frag_row = [&](int j) {   // first LDS row of fragment j inside a stage
-    if (j < 8)
-      return MODE == kGated ? (j >> 2) * 128 + wn * 64 + (j & 3) * 16 : wn * 128 + j * 16;
-    return G_BM + wm * 128 + (j - 8) * 16;   // token rows follow the 256 weight rows
+  auto frag_row = [&](int j) {
+    if (j < 4)
+      return MODE == kGated ? (j >> 1) * 128 + wn * 32 + (j & 1) * 16 : wn * 64 + j * 16;
+    return G_BM + wm * 128 + (j - 4) * 16;
   };
-  auto read_one = [&](int s, int q, int j, frag (&fa)[8], frag (&fb)[8]) {
-    const char* a = smem + (s & (G_NST - 1)) * G_STAGE + rd[q] + frag_row(j) * G_ROW;
-    if (j < 8) fa[j] = *(const frag*)a;
-    else fb[j - 8] = *(const frag*)a;
+  auto read_a = [&](int s, int q, int j, frag (&fa)[4]) {
+    fa[j] = *(const frag*)(smem + (s & (G_NST - 1)) * G_STAGE + rd[q] + frag_row(j) * G_ROW);
+  };
+  auto read_b = [&](int s, int q, int t, frag (&fb)[8]) {
+    fb[t] = *(const frag*)(smem + (s & (G_NST - 1)) * G_STAGE + rd[q] + frag_row(4 + t) * G_ROW);
   };
 
-  f32x4 acc[8][8];
+  f32x4 acc[4][8];
 #pragma unroll
-  for (int f = 0; f < 8; ++f)
+  for (int f = 0; f < 4; ++f)
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[f][t][e] = 0.0f;
 
-  // The 64 matrix instructions of step q of slice s (fragments fa / fb), each followed by a
-  // share of the other work: the 16 fragment reads of the next step (slice rs, step rq; one
-  // per 4 instructions, into na / nb) and, with DMA, the 16 loads of slice s + 2 into the
-  // buffer slice s leaves (one per 4), so neither the LDS nor the address unit sees a burst.
-  auto step = [&](int s, const frag (&fa)[8], const frag (&fb)[8], int rs, int rq, frag (&na)[8],
-                  frag (&nb)[8], auto dma) {
+  // One 32-wide step: 32 matrix instructions token-block major; each token fragment is
+  // reloaded for the next step (slice rs, step rq) right after its last use, the next
+  // weight fragments go into the other set early, and with DMA the 8 refill loads of slice
+  // s + 2 are spread one per 4 instructions.
+  frag fa0[4], fa1[4], fb[8];
+  auto step = [&](int s, const frag (&fa)[4], int rs, int rq, frag (&na)[4], auto dma) {
 #pragma unroll
-    for (int f = 0; f < 8; ++f)
+    for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int i = f * 8 + t;
+      for (int f = 0; f < 4; ++f) {
+        const int i = t * 4 + f;
         acc[f][t] = GMfma<T>::run(fa[f], fb[t], acc[f][t]);
-        if ((i & 3) == 0) read_one(rs, rq, i >> 2, na, nb);
+        if (f == 3) read_b(rs, rq, t, fb);
+        if ((i & 3) == 1 && i < 16) read_a(rs, rq, i >> 2, na);
         if constexpr (decltype(dma)::value) {
           if ((i & 3) == 2) issue_one(s + G_NST, i >> 2);
         }
@@ -285,12 +281,6 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
       }
   };
 
-  // Two stages.  Per slice s: step 0 reads the fragments of step 1; then one barrier (slice
-  // s + 1 has landed, every wave has read all of slice s); step 1 reads the first fragments
-  // of slice s + 1 and refills the buffer of slice s with slice s + 2, which then has a whole
-  // step before it is needed.  Slices at or past KT load as zeros, so the loop runs
-  // uniformly and its last refills and reads are harmless.
-  frag fa0[8], fb0[8], fa1[8], fb1[8];
 #pragma unroll
   for (int s = 0; s < G_NST; ++s)
 #pragma unroll
@@ -298,25 +288,26 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
   wait_vmcnt<2 * G_LOADS>();
   barrier_no_fence();
 #pragma unroll
-  for (int j = 0; j < 16; ++j) read_one(0, 0, j, fa0, fb0);
+  for (int j = 0; j < 4; ++j) read_a(0, 0, j, fa0);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) read_b(0, 0, t, fb);
   __builtin_amdgcn_sched_barrier(0);
   for (int s = 0; s < KT; ++s) {
-    step(s, fa0, fb0, s, 1, fa1, fb1, std::integral_constant<bool, false>());
-    wait_vmcnt<0>();                     // slice s + 1 is in
-    __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's reads of slice s are done
+    step(s, fa0, s, 1, fa1, std::integral_constant<bool, false>());
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
     barrier_no_fence();
     __builtin_amdgcn_sched_barrier(0);
-    step(s, fa1, fb1, s + 1, 0, fa0, fb0, std::integral_constant<bool, true>());
+    step(s, fa1, s + 1, 0, fa0, std::integral_constant<bool, true>());
   }
-  wait_vmcnt<0>();   // the last refills (zeros) land before the LDS is used again
+  wait_vmcnt<0>();
 
-  // epilogue: block (f, t) holds, in lane l, token column t * 16 + (l & 15) and the 4
-  // consecutive weight rows f * 16 + 4 * (l >> 4) .. + 3
+  // epilogue: block (f, t) holds token t * 16 + (l & 15) and weight rows f * 16 + 4 (l >> 4) ..
   const int q4 = lane >> 4;
   const bool vec = p.vec_out != 0;
   T* y = (T*)p.y;
-  constexpr int NF = MODE == kGated ? 4 : 8;   // output column blocks of 16 per wave
-  constexpr int NCOL = NF * 16;                // output columns of a wave
+  constexpr int NF = MODE == kGated ? 2 : 4;   // output column blocks of 16 per wave
+  constexpr int NCOL = NF * 16;
   const int col0 = n0 + wn * NCOL;
   auto values = [&](int f, int t, const float (&bgv)[4], const float (&buv)[4], float (&v)[4],
                     auto bias) {
@@ -324,27 +315,22 @@ __global__ __launch_bounds__(G_THREADS, 1) void gemm_mfma_kernel(const GemmParam
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       gv[j] = acc[f][t][j];
-      uv[j] = MODE == kGated ? acc[f + 4][t][j] : 0.0f;
+      uv[j] = MODE == kGated ? acc[f + 2][t][j] : 0.0f;
     }
     finish4<T, MODE, ACT, decltype(bias)::value, float>(gv, uv, bgv, buv, v);
   };
   if (p.vec_out == 2) {
-    // Staged through LDS (free once every wave has read its last fragments): each wave
-    // writes its 128 x NCOL output block into its own LDS region, then stores whole rows,
-    // 16 bytes per lane, so every cache line of y is written by one instruction.
-    constexpr int RB = NCOL * 2;           // bytes of a staged row
-    constexpr int CPR = RB / 16;           // 16-byte chunks per row
-    constexpr int RPI = 64 / CPR;          // rows per store instruction
-    // chunk swizzle of a staged row: the 16 rows one write instruction touches spread over
-    // distinct bank groups
-    auto row_swz = [](int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); };
+    constexpr int RB = NCOL * 2;
+    constexpr int CPR = RB / 16;
+    constexpr int RPI = 64 / CPR;
+    auto row_swz = [](int r) { return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3); };
     __builtin_amdgcn_s_waitcnt(kLgkm0);
     barrier_no_fence();
     char* stage = smem + wave * (128 * RB);
     auto to_lds = [&](auto bias) {
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
-        const int c4 = f * 16 + 4 * q4;   // first of the lane's 4 columns in the wave block
+        const int c4 = f * 16 + 4 * q4;
         float bgv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, buv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (decltype(bias)::value) {
           bias4<T, float>(p.bg, col0 + c4, p.N, true, bgv);
