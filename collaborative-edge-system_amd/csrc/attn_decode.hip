@@ -127,24 +127,19 @@ __global__ __launch_bounds__(DTHREADS) void decode_vis_kernel(const DecodeParams
   const int nkeys = min(p.chunk, p.Sk[part] - key0);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int total_chunks = p.chunk_begin[p.nparts];
-  __shared__ int64_t qp[16];
   __shared__ uint32_t wmask[NW];
-  if (tid < p.Sq) qp[tid] = p.q_pos[b * p.qps_b + (int64_t)tid * p.qps_s];
-  __syncthreads();
+  // every load is issued before the first wait (key indices clamped into the chunk)
   const int64_t* kp = p.k_pos[part] + b * p.kps[part][0];
   const int64_t kps = p.kps[part][1];
-  uint32_t words[4];
+  int64_t pk[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int k = tid * 4 + u;
-    uint32_t w = 0;
-    if (k < nkeys) {
-      const int64_t pk = kp[(int64_t)(key0 + k) * kps];
-      if (pk >= 0)
-        for (int q = 0; q < p.Sq; ++q)
-          if (!p.causal || pk <= qp[q]) w |= 1u << q;
-    }
-    words[u] = w;
+  for (int u = 0; u < 4; ++u) pk[u] = kp[(int64_t)(key0 + min(tid * 4 + u, nkeys - 1)) * kps];
+  uint32_t words[4] = {0u, 0u, 0u, 0u};
+  for (int q = 0; q < p.Sq; ++q) {
+    const int64_t qs = p.q_pos[b * p.qps_b + (int64_t)q * p.qps_s];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (tid * 4 + u < nkeys && pk[u] >= 0 && (!p.causal || pk[u] <= qs)) words[u] |= 1u << q;
   }
   if (tid * 4 < p.chunk) {
     uint2 packed = {words[0] | (words[1] << 16), words[2] | (words[3] << 16)};
@@ -181,22 +176,36 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int total_chunks = p.chunk_begin[p.nparts];
   float* part_out = p.partial + (((int64_t)b * p.Hkv + kvh) * total_chunks + chunk) * NR * (D + 2);
-  const uint64_t mask = p.tile_mask[(int64_t)b * total_chunks + chunk];
-  if (mask == 0) {  // no key of the chunk is visible to any query row
-    if (tid < NR) {
-      part_out[tid * (D + 2) + D] = -__builtin_inff();
-      part_out[tid * (D + 2) + D + 1] = 0.f;
-    }
-    return;
-  }
-  const int part = part_of(p, chunk);
-  const int Sk = p.Sk[part];
-  const int key0 = (chunk - p.chunk_begin[part]) * p.chunk;
   const int row = lane & 15;   // query row (MFMA column) of this lane
   const int grp = lane >> 4;   // 4-key group of the 16-key tile
   const int G = p.G;
   const bool row_real = row < p.Sq * G;
   const int qbit = row / G;    // query index s of this row
+  char* wb = dsmem + wave * L::WAVE_BYTES;
+
+  // ---- the query rows r = s * G + g of this kv head come straight into the wave's first tile
+  // buffer (free until the first tile load), in flight together with the chunk's tile mask, so
+  // the workgroup starts streaming after one memory round trip
+  {
+    constexpr int QLOADS = NR * D * 2 <= 1024 ? 1 : NR * D * 2 / 1024;
+    const i32x4 qrs = make_rsrc((const T*)p.q + b * p.qs_b,
+                                (uint32_t)((((int64_t)p.Sq - 1) * p.qs_s + ((int64_t)p.Hq - 1) * p.qs_h + D) * sizeof(T)));
+#pragma unroll
+    for (int i = 0; i < QLOADS; ++i) {
+      const int r = i * 4 + (lane >> 4);
+      const int rr = r < p.Sq * G ? r : 0;  // padding rows read row 0 (zeroed below)
+      const uint32_t off = (uint32_t)(((int64_t)(rr / G) * p.qs_s + (int64_t)(kvh * G + rr % G) * p.qs_h) * sizeof(T)) +
+                           (lane & 15) * 16;
+      buffer_load_lds16(qrs, wb + i * 1024, off);
+    }
+  }
+  const uint64_t mask = p.tile_mask[(int64_t)b * total_chunks + chunk];
+  wait_vmcnt<0>();  // query rows in LDS (also before an early exit frees the LDS)
+  // no key of the chunk is visible to any query row: no partial (the reduction reads the mask)
+  if (mask == 0) return;
+  const int part = part_of(p, chunk);
+  const int Sk = p.Sk[part];
+  const int key0 = (chunk - p.chunk_begin[part]) * p.chunk;
 
   // ---- this lane's Q fragments (B operand of S = K.Q^T), sign folded for a negative scale
   const float scale = (float)p.scale;
@@ -205,20 +214,17 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   const uint32_t flip = scale < 0.f ? 0x80008000u : 0u;
   frag8 qf[D / 32];
   {
-    // padding rows (row >= Sq*G) read query row 0 and zero it
-    const int qr = row_real ? row : 0;
-    const T* qrow = (const T*)p.q + b * p.qs_b + (int64_t)(qr / G) * p.qs_s + (kvh * G + qr % G) * p.qs_h;
-    u32x4 raw[D / 32];
-#pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) raw[ks] = *(const u32x4*)(qrow + ks * 32 + grp * 8);
+    const char* qs = wb + (row_real ? row : 0) * (D * 2);
     const uint32_t keep = row_real ? 0xffffffffu : 0u;
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
+      u32x4 raw = *(const u32x4*)(qs + ks * 64 + grp * 16);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) raw[ks][w] = (raw[ks][w] ^ flip) & keep;
-      __builtin_memcpy(&qf[ks], &raw[ks], 16);
+      for (int w = 0; w < 4; ++w) raw[w] = (raw[w] ^ flip) & keep;
+      __builtin_memcpy(&qf[ks], &raw, 16);
     }
   }
+  wait_lgkmcnt0();  // Q in registers before the first tile load overwrites the buffer
 
   // ---- per-lane constant offsets
   const char* kbase = (const char*)((const T*)p.k[part] + b * p.ks[part][0] + kvh * p.ks[part][2]);
@@ -245,7 +251,6 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
       v_raddr[dt] = L::TILE_BYTES + vr * L::ROW + ((dt ^ (vr & 7)) << 5) + 8 * (row & 3);
   }
 
-  char* wb = dsmem + wave * L::WAVE_BYTES;
   // this wave's tiles: wave, wave + NW, ... that hold a visible key
   uint64_t todo = mask & (0x1111111111111111ull << wave);
   auto pop_tile = [&]() -> int {
@@ -327,10 +332,6 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   // ---- per-wave stream over its tiles: two buffers, refilled as soon as their fragments are
   // in registers, so two tiles are in flight during the math of a third
   {
-    // Q in registers first: the compiler's wait for it at its first use would otherwise also
-    // drain the tile loads issued by then
-#pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) asm volatile("" ::"v"(qf[ks]));
     int t = pop_tile();
     int t1 = pop_tile();
     int buf = 0;
@@ -385,10 +386,12 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
         Lsum = __builtin_fmaf(red_l[w][r], wt, Lsum);
       }
     }
-    part_out[r * (D + 2) + d] = acc;
+    // non-temporal stores: written back past the caches' keep-set, they disturb the K/V read
+    // stream of the other workgroups far less than ordinary write-backs do
+    __builtin_nontemporal_store(acc, part_out + r * (D + 2) + d);
     if (d == 0) {
-      part_out[r * (D + 2) + D] = M;
-      part_out[r * (D + 2) + D + 1] = Lsum;
+      __builtin_nontemporal_store(M, part_out + r * (D + 2) + D);
+      __builtin_nontemporal_store(Lsum, part_out + r * (D + 2) + D + 1);
     }
   }
 }
@@ -404,6 +407,7 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
 constexpr int RTHREADS = 256;
 constexpr int RWAVES = RTHREADS / 64;
 constexpr int RCH = kDecodeMaxChunks;  // chunks staged per row
+constexpr int RPF = 12;                // chunk outputs per wave read ahead of their weights
 
 __device__ __forceinline__ float block_max(float v, float* red) {
 #pragma unroll
@@ -449,9 +453,21 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   __shared__ float red[RWAVES];
   __shared__ float2 acc_s[RWAVES][D / 2];
 
+  // the first chunk outputs of this wave, read now so their latency overlaps the statistics
+  // (chunks past the end read chunk 0; unused)
+  float2 pre[RPF];
+#pragma unroll
+  for (int k = 0; k < RPF; ++k) {
+    const int j = wave + RWAVES * k;
+    pre[k] = total > 0 ? *(const float2*)(base + (j < total ? j : 0) * cstride + 2 * lane) : float2{0.f, 0.f};
+  }
+  // chunks without a visible key wrote no partial: their weight is 0
+  const uint64_t* cmask = p.tile_mask + (int64_t)b * total;
   for (int j = tid; j < total; j += RTHREADS) {
-    m_s[j] = base[j * cstride + D];
-    w_s[j] = base[j * cstride + D + 1];  // l, replaced by the weight below
+    const bool live = cmask[j] != 0;
+    const float mv = base[j * cstride + D], lv = base[j * cstride + D + 1];
+    m_s[j] = live ? mv : -__builtin_inff();
+    w_s[j] = live ? lv : 0.f;  // l, replaced by the weight below
   }
   __syncthreads();
   float lse_p[CEA_MAX_PARTS];
@@ -484,13 +500,22 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
     w_s[j] = (empty || m_s[j] == -__builtin_inff()) ? 0.f : expf(m_s[j] - lse);
   __syncthreads();
 
-  // weighted sum of the chunk outputs over [c0, c1): wave w takes chunks c0 + w, c0 + w + 4, ...
+  // weighted sum of the chunk outputs over [c0, c1): wave w takes chunks w, w + 4, ...; the
+  // first RPF of them came in with the statistics (pre), later ones are read when their weight
+  // is known (a chunk of weight 0 is never read or used: it may hold no partial)
   auto chunk_sum = [&](int c0, int c1) -> float2 {
     float2 a = {0.f, 0.f};
-#pragma unroll 8
-    for (int j = c0 + wave; j < c1; j += RWAVES) {
-      // chunks without a visible key have weight 0 and unwritten outputs: they are not read
-      // (the weight is the same for the whole wave, so the load is skipped, not masked)
+#pragma unroll
+    for (int k = 0; k < RPF; ++k) {
+      const int j = wave + RWAVES * k;
+      if (j >= c0 && j < c1) {
+        const float w = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(w_s[j])));
+        a.x = w != 0.f ? __builtin_fmaf(pre[k].x, w, a.x) : a.x;
+        a.y = w != 0.f ? __builtin_fmaf(pre[k].y, w, a.y) : a.y;
+      }
+    }
+    const int j0 = wave + RWAVES * RPF;
+    for (int j = j0 + ((c0 > j0 ? c0 - j0 + RWAVES - 1 : 0) / RWAVES) * RWAVES; j < c1; j += RWAVES) {
       const float w = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(w_s[j])));
       if (w != 0.f) {
         const float2 o = *(const float2*)(base + j * cstride + 2 * lane);
