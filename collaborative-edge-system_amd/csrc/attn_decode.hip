@@ -397,10 +397,11 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
 }
 
 // Reduction of the chunk partials, one workgroup of RTHREADS per (b, s, h) output row.
-//   1. the (m, l) of every chunk into LDS;
-//   2. per partition: M_p = max m, L_p = sum l * exp(m - M_p), lse_p = M_p + log L_p; then
-//      lse = logsumexp over partitions (the reference merge's formula) and per-chunk weights
-//      W = exp(m - lse), which fold a chunk's partition normalisation and its merge weight;
+//   1. the (m, l) of every chunk into LDS, the first chunk outputs into registers;
+//   2. in one wave: per partition M_p = max m, L_p = sum l * exp(m - M_p), lse_p = M_p +
+//      log L_p; then lse = logsumexp over partitions (the reference merge's formula) and
+//      per-chunk weights W = exp(m - lse), which fold a chunk's partition normalisation and
+//      its merge weight;
 //   3. out = sum over chunks of o * W, the waves taking interleaved chunks (all loads of a
 //      row independent), combined in a fixed order.  Partition outputs, when requested, are
 //      the same sums restricted to a partition, times exp(lse - lse_p).
@@ -408,31 +409,6 @@ constexpr int RTHREADS = 256;
 constexpr int RWAVES = RTHREADS / 64;
 constexpr int RCH = kDecodeMaxChunks;  // chunks staged per row
 constexpr int RPF = 12;                // chunk outputs per wave read ahead of their weights
-
-__device__ __forceinline__ float block_max(float v, float* red) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float r = red[0];
-#pragma unroll
-  for (int i = 1; i < RWAVES; ++i) r = fmaxf(r, red[i]);
-  return r;
-}
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float r = red[0];
-#pragma unroll
-  for (int i = 1; i < RWAVES; ++i) r += red[i];
-  return r;
-}
 
 template <typename O, int D, int NR>
 __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodeParams p) {
@@ -450,7 +426,6 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
 
   __shared__ float m_s[RCH];
   __shared__ float w_s[RCH];
-  __shared__ float red[RWAVES];
   __shared__ float2 acc_s[RWAVES][D / 2];
 
   // the first chunk outputs of this wave, read now so their latency overlaps the statistics
@@ -470,35 +445,49 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
     w_s[j] = live ? lv : 0.f;  // l, replaced by the weight below
   }
   __syncthreads();
-  float lse_p[CEA_MAX_PARTS];
-  for (int part = 0; part < p.nparts; ++part) {
-    const int c0 = p.chunk_begin[part], c1 = p.chunk_begin[part + 1];
-    float mx = -__builtin_inff();
-    for (int j = c0 + tid; j < c1; j += RTHREADS) mx = fmaxf(mx, m_s[j]);
-    const float M = block_max(mx, red);
-    float l = 0.f;
-    if (M != -__builtin_inff())
-      for (int j = c0 + tid; j < c1; j += RTHREADS)
-        if (m_s[j] != -__builtin_inff()) l = __builtin_fmaf(w_s[j], expf(m_s[j] - M), l);
-    const float L = block_sum(l, red);
-    lse_p[part] = L > 0.f ? M + logf(L) : -__builtin_inff();
+  // statistics in wave 0 alone (wave shuffles, no workgroup barriers): per partition
+  // M_p = max m, L_p = sum l * exp(m - M_p), lse_p = M_p + log L_p; lse = logsumexp over the
+  // partitions (the reference merge's formula); chunk weights exp(m - lse)
+  __shared__ float s_lse[CEA_MAX_PARTS + 1];
+  if (wave == 0) {
+    float lp[CEA_MAX_PARTS];
+    for (int part = 0; part < p.nparts; ++part) {
+      const int c0 = p.chunk_begin[part], c1 = p.chunk_begin[part + 1];
+      float mx = -__builtin_inff();
+      for (int j = c0 + lane; j < c1; j += 64) mx = fmaxf(mx, m_s[j]);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      float l = 0.f;
+      if (mx != -__builtin_inff())
+        for (int j = c0 + lane; j < c1; j += 64)
+          if (m_s[j] != -__builtin_inff()) l = __builtin_fmaf(w_s[j], expf(m_s[j] - mx), l);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off, 64);
+      lp[part] = l > 0.f ? mx + logf(l) : -__builtin_inff();
+    }
+    float lse;
+    if (p.nparts == 1) {
+      lse = lp[0];
+    } else {
+      float mx = -__builtin_inff();
+      for (int part = 0; part < p.nparts; ++part) mx = fmaxf(mx, lp[part]);
+      const float shift = is_inf(mx) ? 0.f : mx;
+      float sum = 0.f;
+      for (int part = 0; part < p.nparts; ++part) sum = add_rn(sum, expf(lp[part] - shift));
+      lse = logf(sum) + shift;
+    }
+    const bool empty = lse == -__builtin_inff();
+    for (int j = lane; j < total; j += 64)
+      w_s[j] = (empty || m_s[j] == -__builtin_inff()) ? 0.f : expf(m_s[j] - lse);
+    if (lane == 0) {
+      for (int part = 0; part < p.nparts; ++part) s_lse[part] = lp[part];
+      s_lse[p.nparts] = lse;
+    }
   }
-  float lse;
-  if (p.nparts == 1) {
-    lse = lse_p[0];
-  } else {
-    float mx = -__builtin_inff();
-    for (int part = 0; part < p.nparts; ++part) mx = fmaxf(mx, lse_p[part]);
-    const float shift = is_inf(mx) ? 0.f : mx;
-    float sum = 0.f;
-    for (int part = 0; part < p.nparts; ++part) sum = add_rn(sum, expf(lse_p[part] - shift));
-    lse = logf(sum) + shift;
-  }
-  const bool empty = lse == -__builtin_inff();
-  __syncthreads();  // every thread has read the l values
-  for (int j = tid; j < total; j += RTHREADS)
-    w_s[j] = (empty || m_s[j] == -__builtin_inff()) ? 0.f : expf(m_s[j] - lse);
   __syncthreads();
+  float lse_p[CEA_MAX_PARTS];
+  for (int part = 0; part < p.nparts; ++part) lse_p[part] = s_lse[part];
+  const float lse = s_lse[p.nparts];
 
   // weighted sum of the chunk outputs over [c0, c1): wave w takes chunks w, w + 4, ...; the
   // first RPF of them came in with the statistics (pre), later ones are read when their weight
