@@ -116,6 +116,32 @@ __device__ __forceinline__ int part_of(const DecodeParams& p, int chunk) {
   return part;
 }
 
+// Work items of the split kernel.  Batch rows b < p.pair_rows take pairs of consecutive chunks
+// of a partition (item_begin: prefix of pair items per partition), the remaining rows single
+// chunks (chunk_begin), so the last workgroups of the launch, which set its tail, are short.
+// Item i of row b: its partition, first chunk and chunk count.
+struct DecodeItem {
+  int part, chunk, nch;
+};
+__device__ __forceinline__ DecodeItem item_of(const DecodeParams& p, int b, int item) {
+  DecodeItem it;
+  if (b < p.pair_rows) {
+    int part = 0;
+    while (part + 1 < p.nparts && item >= p.item_begin[part + 1]) ++part;
+    it.part = part;
+    it.chunk = p.chunk_begin[part] + 2 * (item - p.item_begin[part]);
+    it.nch = min(2, p.chunk_begin[part + 1] - it.chunk);
+  } else {
+    it.part = part_of(p, item);
+    it.chunk = item;
+    it.nch = 1;
+  }
+  return it;
+}
+__device__ __forceinline__ int items_of_row(const DecodeParams& p, int b) {
+  return b < p.pair_rows ? p.item_begin[p.nparts] : p.chunk_begin[p.nparts];
+}
+
 // Visibility prepass, one workgroup per (chunk, batch): for every key of the chunk a word whose
 // bit s says whether query s of the batch sees it (k_pos >= 0 and, when causal,
 // k_pos <= q_pos[s]), and for the chunk a mask of the 16-key tiles holding a visible key.
@@ -172,10 +198,29 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   __shared__ float red_m[NW][NR];
   __shared__ float red_l[NW][NR];
 
-  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // 1-D grid: pair items of rows [0, pair_rows), then single-chunk items of the other rows;
+  // item fastest, then kv head, then batch row
   const int total_chunks = p.chunk_begin[p.nparts];
-  float* part_out = p.partial + (((int64_t)b * p.Hkv + kvh) * total_chunks + chunk) * NR * (D + 2);
+  int b, kvh, item;
+  {
+    const int n2 = p.item_begin[p.nparts];
+    const int first = p.pair_rows * p.Hkv * n2;
+    const int id = blockIdx.x;
+    if (id < first) {
+      b = id / (p.Hkv * n2);
+      kvh = (id / n2) % p.Hkv;
+      item = id % n2;
+    } else {
+      const int r = id - first;
+      b = p.pair_rows + r / (p.Hkv * total_chunks);
+      kvh = (r / total_chunks) % p.Hkv;
+      item = r % total_chunks;
+    }
+  }
+  const DecodeItem it = item_of(p, b, item);
+  const int part = it.part, chunk = it.chunk, nch = it.nch;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  float* part_out = p.partial + (((int64_t)b * p.Hkv + kvh) * total_chunks + item) * NR * (D + 2);
   const int row = lane & 15;   // query row (MFMA column) of this lane
   const int grp = lane >> 4;   // 4-key group of the 16-key tile
   const int G = p.G;
@@ -200,10 +245,10 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
     }
   }
   const uint64_t mask = p.tile_mask[(int64_t)b * total_chunks + chunk];
+  const uint64_t mask1 = nch > 1 ? p.tile_mask[(int64_t)b * total_chunks + chunk + 1] : 0ull;
   wait_vmcnt<0>();  // query rows in LDS (also before an early exit frees the LDS)
-  // no key of the chunk is visible to any query row: no partial (the reduction reads the mask)
-  if (mask == 0) return;
-  const int part = part_of(p, chunk);
+  // no key of the item is visible to any query row: no partial (the reduction reads the masks)
+  if ((mask | mask1) == 0) return;
   const int Sk = p.Sk[part];
   const int key0 = (chunk - p.chunk_begin[part]) * p.chunk;
 
@@ -251,13 +296,22 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
       v_raddr[dt] = L::TILE_BYTES + vr * L::ROW + ((dt ^ (vr & 7)) << 5) + 8 * (row & 3);
   }
 
-  // this wave's tiles: wave, wave + NW, ... that hold a visible key
+  // this wave's tiles: wave, wave + NW, ... that hold a visible key (tile t of the item is
+  // tile t % tpc of its chunk t / tpc; tpc is a multiple of NW, so the lane pattern is the same
+  // in both chunks of a pair)
+  const int tpc = p.chunk / TK;
   uint64_t todo = mask & (0x1111111111111111ull << wave);
+  uint64_t todo1 = mask1 & (0x1111111111111111ull << wave);
   auto pop_tile = [&]() -> int {
-    if (todo == 0) return -1;
-    const int t = (int)__builtin_ctzll(todo);
-    todo &= todo - 1;
-    return t;
+    if (todo != 0) {
+      const int t = (int)__builtin_ctzll(todo);
+      todo &= todo - 1;
+      return t;
+    }
+    if (todo1 == 0) return -1;
+    const int t = (int)__builtin_ctzll(todo1);
+    todo1 &= todo1 - 1;
+    return tpc + t;
   };
   auto load_tile = [&](int t, int buf) {
     const int k0 = key0 + t * TK;
@@ -420,9 +474,11 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kvh = p.map.kv_of(h);
   const int r = s * p.G + (h - kvh * p.G);
-  const int total = p.chunk_begin[p.nparts];
+  const int total_chunks = p.chunk_begin[p.nparts];
+  const int total = items_of_row(p, b);  // work items (partials) of this batch row
+  const int* ibegin = b < p.pair_rows ? p.item_begin : p.chunk_begin;
   const int64_t cstride = (int64_t)NR * (D + 2);
-  const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * total * cstride + r * (D + 2);
+  const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * total_chunks * cstride + r * (D + 2);
 
   __shared__ float m_s[RCH];
   __shared__ float w_s[RCH];
@@ -436,10 +492,11 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
     const int j = wave + RWAVES * k;
     pre[k] = total > 0 ? *(const float2*)(base + (j < total ? j : 0) * cstride + 2 * lane) : float2{0.f, 0.f};
   }
-  // chunks without a visible key wrote no partial: their weight is 0
-  const uint64_t* cmask = p.tile_mask + (int64_t)b * total;
+  // items without a visible key wrote no partial: their weight is 0
+  const uint64_t* cmask = p.tile_mask + (int64_t)b * total_chunks;
   for (int j = tid; j < total; j += RTHREADS) {
-    const bool live = cmask[j] != 0;
+    const DecodeItem it = item_of(p, b, j);
+    const bool live = (cmask[it.chunk] | (it.nch > 1 ? cmask[it.chunk + 1] : 0ull)) != 0;
     const float mv = base[j * cstride + D], lv = base[j * cstride + D + 1];
     m_s[j] = live ? mv : -__builtin_inff();
     w_s[j] = live ? lv : 0.f;  // l, replaced by the weight below
@@ -452,7 +509,7 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   if (wave == 0) {
     float lp[CEA_MAX_PARTS];
     for (int part = 0; part < p.nparts; ++part) {
-      const int c0 = p.chunk_begin[part], c1 = p.chunk_begin[part + 1];
+      const int c0 = ibegin[part], c1 = ibegin[part + 1];
       float mx = -__builtin_inff();
       for (int j = c0 + lane; j < c1; j += 64) mx = fmaxf(mx, m_s[j]);
 #pragma unroll
@@ -528,7 +585,7 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   if (p.part_out[0]) {
     res = {0.f, 0.f};
     for (int part = 0; part < p.nparts; ++part) {
-      const float2 t = chunk_sum(p.chunk_begin[part], p.chunk_begin[part + 1]);
+      const float2 t = chunk_sum(ibegin[part], ibegin[part + 1]);
       res.x += t.x;
       res.y += t.y;
       if (wave == 0) {
@@ -575,7 +632,8 @@ int launch_nr(const DecodeParams& p, hipStream_t st) {
     const hipError_t e = reserve_lds<decode_split_kernel<T, D, NR>>(DLayout<D>::LDS_BYTES);
     CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "decode: cannot reserve %d bytes of LDS: %s",
                 DLayout<D>::LDS_BYTES, hipGetErrorString(e));
-    hipLaunchKernelGGL((decode_split_kernel<T, D, NR>), dim3(total, p.Hkv, p.B), dim3(DTHREADS),
+    const int64_t grid = ((int64_t)p.pair_rows * p.item_begin[p.nparts] + (int64_t)(p.B - p.pair_rows) * total) * p.Hkv;
+    hipLaunchKernelGGL((decode_split_kernel<T, D, NR>), dim3((unsigned)grid), dim3(DTHREADS),
                        DLayout<D>::LDS_BYTES, st, p);
     CEA_CHECK_LAUNCH("decode_split");
   }
@@ -627,11 +685,24 @@ int decode_plan_chunk(int64_t keys_per_head, int32_t B, int32_t Hkv) {
   return ch;
 }
 
-int launch_attn_decode(const DecodeParams& p, hipStream_t st) {
+int launch_attn_decode(const DecodeParams& params, hipStream_t st) {
+  DecodeParams p = params;
   const int nr = decode_rows(p.Sq, p.G);
   CEA_REQUIRE(p.chunk <= CHMAX && p.chunk % TK == 0, CEA_EINVAL, "decode: bad chunk %d", p.chunk);
   CEA_REQUIRE(p.chunk_begin[p.nparts] <= kDecodeMaxChunks, CEA_EUNSUPPORTED,
               "decode: %d chunks exceed %d", p.chunk_begin[p.nparts], kDecodeMaxChunks);
+  // Pair items (half the partials written while K/V stream: those writes cost the read stream
+  // far more than their size) once chunks are at their largest and plentiful.  The last batch
+  // rows keep single chunks: enough of them for about two rounds of resident workgroups (two
+  // per compute unit), so the launch ends on short workgroups.
+  p.item_begin[0] = 0;
+  for (int i = 0; i < p.nparts; ++i)
+    p.item_begin[i + 1] = p.item_begin[i] + (p.chunk_begin[i + 1] - p.chunk_begin[i] + 1) / 2;
+  const int64_t row_items = (int64_t)p.Hkv * p.chunk_begin[p.nparts];
+  const bool pairs = p.chunk == CHMAX && p.B * row_items >= CEA_DECODE_ITEMS;
+  const int cus = device_cus();
+  const int64_t tail_rows = row_items > 0 ? (4 * (int64_t)(cus > 0 ? cus : 256) + row_items - 1) / row_items : 1;
+  p.pair_rows = pairs ? (int)max((int64_t)0, (int64_t)p.B - tail_rows) : 0;
   if (p.D == 128 && p.in_dtype == CEA_BF16) return launch_d<bf16, 128>(p, nr, st);
   if (p.D == 128 && p.in_dtype == CEA_F16) return launch_d<f16, 128>(p, nr, st);
   set_error("decode: unsupported dtype %s / head size %d", dtype_name(p.in_dtype), p.D);

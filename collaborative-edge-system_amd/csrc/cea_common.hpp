@@ -54,6 +54,21 @@ hipError_t reserve_lds(int bytes) {
   return e;
 }
 
+// Compute units of the current device (queried once per device; 0 on error).
+inline int device_cus() {
+  static std::atomic<int> cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) {
+    const int c = cus[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) cus[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 inline size_t dtype_size(int32_t dt) {
   switch (dt) {
     case CEA_F32: return 4;

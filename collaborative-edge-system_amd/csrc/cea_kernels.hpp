@@ -71,6 +71,10 @@ struct DecodeParams {
   int64_t kps[CEA_MAX_PARTS][2];
   int32_t chunk_begin[CEA_MAX_PARTS + 1];  // prefix sum of key chunks per partition
   int32_t chunk;                            // keys per chunk
+  // set by the launcher: rows b < pair_rows take pairs of chunks as work items, item_begin is
+  // the prefix sum of those pair items per partition
+  int32_t pair_rows;
+  int32_t item_begin[CEA_MAX_PARTS + 1];
   double scale;
   int32_t causal;
   int32_t in_dtype;
