@@ -108,6 +108,26 @@ def test_kv_decode_full_batch_against_oracle(cea, dev):
         assert (bf_c[sl].float() - rb.float()).abs().max().item() <= 2e-2, f"decode seq {b} bf16"
 
 
+def test_kv_decode_full_batch_partition_outputs(cea, dev):
+    """Each partition's (out, lse) of the full distributed-KV decode workload (every rank's
+    attention_with_lse, sequence_parallel.py:262-269) against the oracle, on sequences from
+    the batch rows that take pairs of chunks per work item and from the last rows, which take
+    single chunks."""
+    w = cea.workloads.kv_decode(device="cpu")
+    qd, qpd = w.q.to(dev), w.q_pos.to(dev)
+    parts_d = [(k.to(dev), v.to(dev), p.to(dev)) for k, v, p in w.partitions()]
+    out, lse, per = cea.partitioned_attention(qd, qpd, parts_d, return_lse=True, return_parts=True)
+    torch.cuda.synchronize()
+    per_c = [(o.cpu(), l.cpu()) for o, l in per]
+    cpu_parts = w.partitions()
+    for b in (0, 9, 17, 26, 28, 29, 31):
+        sl = slice(b, b + 1)
+        pb = [(k[sl], v[sl], p[sl]) for k, v, p in cpu_parts]
+        _, _, partial = sp_ref.distributed_kv_share(w.q[sl], w.q_pos[sl], pb, with_parts=True)
+        for i, ((po, pl), (ro, rl)) in enumerate(zip(per_c, partial)):
+            assert_attention_close(po[sl], pl[sl], ro, rl, torch.bfloat16, f"decode seq {b} partition {i}")
+
+
 def test_ulysses_share_full_size(cea, dev):
     """The Ulysses local attention (65536 tokens, right padding) against the oracle on 1088
     query rows: 1024 spread evenly over the valid tokens of the packed sequences, 64 in the
