@@ -7,25 +7,30 @@
 // device and in three launches.
 //
 // HBM-bound design:
-//   * work item = (batch, kv head, key chunk of one partition); the NR = Sq*G query rows that
-//     share the kv head (G query heads per kv head) are the columns of 16 x 16 matrix-core
-//     tiles, so each K/V row is read from HBM once for all of them and the arithmetic stays
-//     off the vector ALU: S = K.Q^T with v_mfma_f32_16x16x32 (a lane holds 4 keys of one
-//     query row) and O^T += V^T.P^T with v_mfma_f32_16x16x16 (P is the score tile as is);
+//   * work item = (batch, kv head, one or two consecutive key chunks of one partition); the
+//     NR = Sq*G query rows that share the kv head (G query heads per kv head) are the columns
+//     of 16 x 16 matrix-core tiles, so each K/V row is read from HBM once for all of them and
+//     the arithmetic stays off the vector ALU: S = K.Q^T with v_mfma_f32_16x16x32 (a lane
+//     holds 4 keys of one query row) and O^T += V^T.P^T with v_mfma_f32_16x16x16 (P is the
+//     score tile as is);
 //   * every wave streams its own 16-key tiles of K and V straight into a private pair of LDS
 //     buffers (non-temporal buffer_load ... lds, explicit vmcnt waits, no barriers); a buffer
 //     is refilled as soon as its fragments are in registers, so two tiles stay in flight; V is
 //     read back transposed with ds_read_b64_tr_b16; both tiles are XOR-swizzled so the
-//     fragment and transpose reads are free of LDS bank conflicts;
+//     fragment and transpose reads are free of LDS bank conflicts; the query rows come in by
+//     LDS-DMA as well, together with the item's tile masks;
 //   * a prepass reads the key positions once per batch row (not once per kv head) and turns
 //     them into a 16-bit visibility word per key (bit s: query s sees it) and a mask of the
 //     16-key tiles of each chunk that hold a visible key; the split kernel loads each tile's
-//     words with its K and V, never loads an invisible tile, and leaves a chunk with an empty
-//     mask after one scalar load;
+//     words with its K and V, never loads an invisible tile, and an item with empty masks
+//     writes nothing;
 //   * the waves of a workgroup merge their online-softmax partials in LDS and write one
-//     (o unnormalised, m, l) partial per chunk; the reduction kernel then merges the chunks
-//     (optionally emitting each partition's (out, lse)), computes lse with the reference's
-//     logsumexp over partitions, and writes out (f32 or the query dtype) and lse.
+//     (o unnormalised, m, l) partial per item with non-temporal stores (stores during the
+//     K/V stream cost its read rate far more than their size, so there are as few partial
+//     bytes as the tail allows: pairs of chunks per item except in the last batch rows);
+//   * the reduction kernel merges the items of a row (optionally emitting each partition's
+//     (out, lse)), computes lse with the reference's logsumexp over partitions, and writes
+//     out (f32 or the query dtype) and lse.
 #include "cea_kernels.hpp"
 #include "cea_lds_dma.hpp"
 
