@@ -242,3 +242,42 @@ def test_partitioned_fallback_with_many_chunks(cea, dev):
     ro, rl, _ = sp_ref.distributed_kv_share(q, qpos, parts_cpu, with_parts=True)
     torch.cuda.synchronize()
     assert_attention_close(out, lse, ro.float(), rl, torch.bfloat16, "4 x 300k keys")
+
+
+def test_partitioned_decode_chunk_pairs_two_tokens(cea, dev):
+    """A decode call large enough for the split kernel's chunk pairs (32 rows x 4 kv heads x
+    65 chunks of 1024 keys; the last rows take single chunks), with two new tokens per
+    sequence (8 query rows per kv head): every partition's (out, lse) and the merged result
+    against the oracle on sequences from both kinds of rows.  K / V are drawn on the device;
+    only the checked sequences are copied to the host."""
+    B, Sq, hq, hkv, d, cap = 32, 2, 16, 4, 128, 65536
+    sizes = [39322, cap - 39322]
+    g = torch.Generator(device=dev).manual_seed(21)
+    ck = torch.randn(B, hkv, cap, d, generator=g, device=dev).to(torch.bfloat16)
+    cv = torch.randn(B, hkv, cap, d, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(B, Sq, hq, d, generator=g, device=dev).to(torch.bfloat16)
+    gc = torch.Generator().manual_seed(22)
+    lens = torch.randint(2, cap + 1, (B,), generator=gc)
+    lens[28] = cap  # a full-length sequence among the single-chunk rows
+    slots = torch.arange(cap).view(1, cap)
+    kpos = torch.where(slots < lens.view(-1, 1), slots, torch.full_like(slots, -1))
+    qpos = (lens - 2).view(-1, 1) + torch.arange(Sq).view(1, Sq)
+    kpd, qpd = kpos.to(dev), qpos.to(dev)
+    parts, start = [], 0
+    for n in sizes:
+        parts.append((ck[:, :, start:start + n].transpose(1, 2), cv[:, :, start:start + n].transpose(1, 2),
+                      kpd[:, start:start + n]))
+        start += n
+    out, lse, per = cea.partitioned_attention(q, qpd, parts, return_lse=True, return_parts=True)
+    torch.cuda.synchronize()
+    for b in (0, 5, 13, 27, 28, 31):
+        sl = slice(b, b + 1)
+        pb, start = [], 0
+        for n in sizes:
+            pb.append((ck[sl, :, start:start + n].transpose(1, 2).cpu(), cv[sl, :, start:start + n].transpose(1, 2).cpu(),
+                       kpos[sl, start:start + n]))
+            start += n
+        ro, rl, rparts = sp_ref.distributed_kv_share(q[sl].cpu(), qpos[sl], pb, with_parts=True)
+        for i, ((po, pl), (qo, ql)) in enumerate(zip(per, rparts)):
+            assert_attention_close(po[sl], pl[sl], qo, ql, torch.bfloat16, f"seq {b} partition {i}")
+        assert_attention_close(out[sl], lse[sl], ro.float(), rl, torch.bfloat16, f"seq {b} merged")
