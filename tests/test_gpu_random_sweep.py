@@ -132,3 +132,34 @@ def test_random_partitions_match_oracle(cea, dev, pc):
     assert_attention_close(out, lse, ro, rl, dtype, "merged")
     assert plain.dtype == dtype
     assert (plain.float().cpu() - rb.float()).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("sizes", [[0, 700, 0, 1500], [0, 0], [1024, 0], [0, 3000, 17]],
+                         ids=lambda s: "-".join(map(str, s)))
+def test_partitions_with_empty_ranks(cea, dev, sizes):
+    """Ranks holding no KV yet: an empty partition's attention_with_lse is (0, -inf)
+    (attention.py:152-157) and merges as the identity; with every partition empty the result
+    is (0, -inf) throughout."""
+    B, Sq, Hq, Hkv, D, dtype = 2, 1, 8, 2, 128, torch.bfloat16
+    g = torch.Generator().manual_seed(sum(sizes) + len(sizes))
+    q = torch.randn(B, Sq, Hq, D, generator=g).to(dtype)
+    parts, start = [], 0
+    for n in sizes:
+        parts.append((torch.randn(B, n, Hkv, D, generator=g).to(dtype),
+                      torch.randn(B, n, Hkv, D, generator=g).to(dtype),
+                      (torch.arange(n) + start).repeat(B, 1)))
+        start += n
+    q_pos = torch.full((B, Sq), max(start - 1, 0))
+    print(f"partitions {sizes}", flush=True)
+    pd = [(k.to(dev), v.to(dev), p.to(dev)) for k, v, p in parts]
+    out, lse, per = cea.partitioned_attention(q.to(dev), q_pos.to(dev), pd, return_lse=True,
+                                              return_parts=True)
+    torch.cuda.synchronize()
+    rb, rl, partial = sp_ref.distributed_kv_share(q, q_pos, parts, with_parts=True)
+    for j, ((po, pl), (ro, rlp)) in enumerate(zip(per, partial)):
+        assert_attention_close(po, pl, ro, rlp, dtype, f"partition {j}")
+    ro = partial[0][0] if len(partial) == 1 else ref.merge_many([x[0] for x in partial],
+                                                                 [x[1] for x in partial])[0]
+    assert_attention_close(out, lse, ro, rl, dtype, "merged")
+    if start == 0:
+        assert bool((out == 0).all()) and bool(torch.isinf(lse).all())
