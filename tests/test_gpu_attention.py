@@ -255,3 +255,21 @@ def test_f32_matrix_core_and_generic_paths(cea, dev, D):
     o1, l1 = cea.attention_with_lse(qa[:, -1:], ka, va, qp[:, -1:].to(dev), kp.to(dev))
     torch.cuda.synchronize()
     assert_attention_close(o1, l1, ro[:, -1:], rl[:, :, -1:], torch.float32, f"f32 D{D} decode row")
+
+
+@pytest.mark.parametrize("Sq,Sk", [(5, 0), (0, 7), (0, 0)])
+def test_empty_query_or_key_block(cea, dev, Sq, Sk):
+    """No query rows or no keys: the reference's early empty result (attention.py:152-157),
+    out zeros and lse -inf of the accumulation dtype (plain attention: zeros of q's dtype)."""
+    g = torch.Generator().manual_seed(Sq * 10 + Sk)
+    q = torch.randn(2, Sq, 4, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(2, Sk, 2, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, Sk, 2, 128, generator=g).to(torch.bfloat16)
+    qp, kp = torch.arange(Sq).repeat(2, 1), torch.arange(Sk).repeat(2, 1)
+    out, lse = cea.attention_with_lse(q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev))
+    plain = cea.attention.attention(q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev))
+    torch.cuda.synchronize()
+    ro, rl = ref.attention_with_lse(q, k, v, qp, kp)
+    assert out.shape == ro.shape and out.dtype == ro.dtype and lse.shape == rl.shape
+    assert torch.equal(out.cpu(), ro) and torch.equal(lse.cpu(), rl)
+    assert plain.shape == q.shape and plain.dtype == q.dtype and bool((plain == 0).all())
