@@ -202,3 +202,15 @@ def test_operators_refuse_host_tensors(cea):
         cea.attention_with_lse(q, q, q, pos, pos)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         cea.rmsnorm(q, torch.ones(8), 1e-5)
+
+
+def test_missing_libraries_fail_loudly(cea, monkeypatch, tmp_path):
+    """No fallback: without the built kernel or operator library every entry raises, naming
+    the missing file and how to build it."""
+    nat = cea._native
+    with pytest.raises(RuntimeError, match="missing: build it"):
+        nat.load_library(tmp_path / "libcollab_edge_attn.so")
+    monkeypatch.setattr(nat, "_ops", None)
+    monkeypatch.setattr(nat, "OPS_PATH", tmp_path / "libcollab_edge_torch.so")
+    with pytest.raises(RuntimeError, match="missing: build it"):
+        nat.ops()
