@@ -103,11 +103,12 @@ def _event_timed(fn, steps: int, warmup: int, torch, dev):
 
 
 def bench_ring(cea, torch, steps, warmup, dev):
-    """The headline: ``ring_attention`` over the four KV blocks of the ring share.  The K
-    timed steps are bracketed by host synchronisation (wall clock, ``value``) and by two HIP
-    events on the stream the kernels run on; the events give the GPU time of exactly those
-    steps, from which ``roofline`` takes the average duration of one ring step's attention
-    call (tile-summary pass + prefill kernel with its in-epilogue merge)."""
+    """The headline: ``ring_attention`` over the four KV blocks of the ring share, one
+    ``cea_ring_attention`` call (one tile-summary launch over the four blocks + one prefill
+    launch that streams them in ring order).  The K timed steps are bracketed by host
+    synchronisation (wall clock, ``value``) and by two HIP events on the stream the kernels
+    run on; the events give the GPU time of exactly those steps, from which ``roofline``
+    takes the average duration of one share's launch pair."""
     w = cea.workloads.ring_share(device=dev)
     comm = cea.LocalGroup(w.layout.num_ranks, w.rank)
     for r, (k, v, p) in enumerate(w.blocks):
@@ -129,7 +130,7 @@ def bench_ring(cea, torch, steps, warmup, dev):
     b.record(stream)
     torch.cuda.synchronize()
     sec = (time.perf_counter() - t0) / steps
-    n_launch = len(w.ring_order)
+    n_launch = 1  # the whole share is one prefill launch
     launch_ms = a.elapsed_time(b) / (steps * n_launch)
     flop_launch = w.flop / n_launch
     achieved = flop_launch / (launch_ms * 1e-3) / 1e12
@@ -141,7 +142,7 @@ def bench_ring(cea, torch, steps, warmup, dev):
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
         "traffic": _measured_traffic("attn_prefill_ring_share"),
-        "kernel": "attn_prefill_kernel<bf16,128> (+ tile summary pass), one ring step",
+        "kernel": "attn_prefill_kernel<bf16,128> over the 4 KV blocks in ring order (+ tile summary pass), one share",
         "launch_ms": round(launch_ms, 4),
         "launches": steps * n_launch,
         "flop_per_launch": int(flop_launch),

@@ -75,6 +75,17 @@ _SIGNATURES = {
         [_P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_double, ctypes.POINTER(ctypes.c_int32),
          ctypes.c_int32, _P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
     ),
+    "cea_ring_attention_workspace_bytes": (
+        ctypes.c_size_t,
+        [_P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32),
+         ctypes.c_int32, _P, _P],
+    ),
+    "cea_ring_attention": (
+        ctypes.c_int,
+        [_P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_double,
+         ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, _P, _P, ctypes.c_void_p,
+         ctypes.c_size_t, ctypes.c_void_p],
+    ),
     "cea_merge_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
     "cea_merge_attention_list": (ctypes.c_int, [ctypes.c_int32, _P, _P, _P, _P, ctypes.c_void_p]),
     "cea_pack_partial": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p]),

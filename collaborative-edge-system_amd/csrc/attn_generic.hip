@@ -46,6 +46,40 @@ int launch_tile_info(const int64_t* k_pos, int64_t kps_b, int64_t kps_s, int32_t
   return CEA_OK;
 }
 
+// The same summaries for every block of a segment table: tile t of the launch's numbering
+// belongs to the last block whose first tile is <= t.
+__global__ __launch_bounds__(64) void tile_info_segs_kernel(const KvSegs segs, int ntiles,
+                                                            TileInfo* __restrict__ out) {
+  const int t = blockIdx.x, b = blockIdx.y;
+  int s = 0;
+  while (s + 1 < segs.n && t >= segs.seg[s + 1].tile0) ++s;
+  const KvSeg& g = segs.seg[s];
+  const int key = (t - g.tile0) * kTileKeys + threadIdx.x;
+  int64_t p = -1;
+  if (key < g.Sk) p = g.k_pos[b * g.kps_b + (int64_t)key * g.kps_s];
+  const bool valid = p >= 0;
+  const int64_t mn = wave_min_i64(valid ? p : INT64_MAX);
+  const int64_t mx = wave_max_i64(valid ? p : INT64_MIN);
+  const int cnt = wave_sum_i32(valid ? 1 : 0);
+  if (threadIdx.x == 0) {
+    TileInfo ti;
+    ti.min_valid = mn;
+    ti.max_valid = mx;
+    ti.n_valid = cnt;
+    ti.pad[0] = ti.pad[1] = ti.pad[2] = 0;
+    out[(int64_t)b * ntiles + t] = ti;
+  }
+}
+
+int launch_tile_info_segs(const KvSegs& segs, int32_t B, TileInfo* tiles, int32_t ntiles,
+                          hipStream_t st) {
+  if (B == 0 || ntiles == 0) return CEA_OK;
+  CEA_REQUIRE(B < 65536, CEA_EUNSUPPORTED, "attention: batch %d too large", B);
+  hipLaunchKernelGGL(tile_info_segs_kernel, dim3(ntiles, B), dim3(64), 0, st, segs, ntiles, tiles);
+  CEA_CHECK_LAUNCH("tile_info");
+  return CEA_OK;
+}
+
 // ---------------------------------------------------------------------------------------
 // generic attention
 // ---------------------------------------------------------------------------------------

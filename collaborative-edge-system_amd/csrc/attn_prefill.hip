@@ -28,6 +28,8 @@
 //     each wave then computes a tile unmasked, element-masked or not at all from its own
 //     query-position range, so causal, zigzag and padding masks cost nothing on tiles that
 //     are entirely visible or entirely hidden.
+#include <string.h>
+
 #include "cea_kernels.hpp"
 #include "cea_lds_dma.hpp"
 
@@ -121,12 +123,16 @@ template <int LPT> __device__ __forceinline__ void wait_tiles_ahead(int ahead) {
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnParams p) {
+// MULTI: the launch streams several KV blocks (segs.n > 1); otherwise block 0 only, whose
+// addresses the compiler keeps in registers for the whole kernel.
+template <typename T, int D, bool MULTI>
+__global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnParams p,
+                                                                   const KvSegs segs) {
   typedef Layout<D> L;
   typedef typename Mfma<T>::frag frag;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  // listed tiles: (tile index, 2-bit mode of every wave: 0 skip, 1 full, 2 element-masked)
+  // listed tiles: (block << 24 | tile of the block, 2-bit mode of every wave: 0 skip, 1 full,
+  // 2 element-masked)
   __shared__ int2 tile_list[LIST_CAP];
   __shared__ int64_t red_q[NWAVES], red_qmin[NWAVES];
   __shared__ int red_act[NWAVES];
@@ -187,9 +193,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     }
   }
 
-  const char* kbase = (const char*)((const T*)p.k + b * p.ks_b + kvh * p.ks_h);
-  const char* vbase = (const char*)((const T*)p.v + b * p.vs_b + kvh * p.vs_h);
-  const char* pbase = (const char*)(p.k_pos + b * p.kps_b);
+  // tile summaries of all blocks, numbered block after block
   const TileInfo* tinfo = p.tiles + (int64_t)b * p.ntiles;
   const uint32_t krow_bytes = (uint32_t)(p.ks_s * 2), vrow_bytes = (uint32_t)(p.vs_s * 2);
 
@@ -226,18 +230,34 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   const uint32_t smem_lds = lds_addr(smem);
   const uint32_t wave_kv = __builtin_amdgcn_readfirstlane(wave) * (L::KV_LOADS * 1024);
   const uint32_t wave_pos = __builtin_amdgcn_readfirstlane(wave) * 64;
-  auto load_tile = [&](int t, int stage) {
-    const int key0 = t * BN;
-    const int left = p.Sk - key0;  // > 0 for every listed tile
-    const auto krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, (uint32_t)(left - 1) * krow_bytes + L::KROW);
-    const auto vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, (uint32_t)(left - 1) * vrow_bytes + L::KROW);
+  // block of a list entry (block << 24 | tile): a compile-time 0 for single-block launches
+  auto seg_of = [&](int x) -> const KvSeg& { return segs.seg[MULTI ? (x >> 24) : 0]; };
+  // buffer sources of one tile, worked out a step before its loads are issued (the block's
+  // pointers come from kernel arguments; for several blocks that is a dependent scalar load)
+  struct TileSrc {
+    i32x4 krs, vrs, prs;
+  };
+  auto tile_src = [&](int x) {
+    const KvSeg& sg = seg_of(x);
+    const int key0 = (x & 0xffffff) * BN;
+    const int left = sg.Sk - key0;  // > 0 for every listed tile
+    const char* kbase = (const char*)((const T*)sg.k + b * sg.ks_b + kvh * sg.ks_h);
+    const char* vbase = (const char*)((const T*)sg.v + b * sg.vs_b + kvh * sg.vs_h);
+    const char* pbase = (const char*)(sg.k_pos + b * sg.kps_b);
+    TileSrc ts;
+    ts.krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, (uint32_t)(left - 1) * krow_bytes + L::KROW);
+    ts.vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, (uint32_t)(left - 1) * vrow_bytes + L::KROW);
+    ts.prs = make_rsrc(pbase + (int64_t)key0 * 8, (uint32_t)left * 8);
+    return ts;
+  };
+  auto load_tile = [&](const TileSrc& ts, int stage) {
+    const i32x4 krs = ts.krs, vrs = ts.vrs, prs = ts.prs;
     const uint32_t st = smem_lds + stage * L::STAGE_BYTES;
 #pragma unroll
     for (int i = 0; i < L::KV_LOADS; ++i) buffer_load_lds16_m0(krs, st + wave_kv + i * 1024, k_voff[i]);
 #pragma unroll
     for (int i = 0; i < L::KV_LOADS; ++i)
       buffer_load_lds16_m0(vrs, st + L::K_BYTES + wave_kv + i * 1024, v_voff[i]);
-    const auto prs = make_rsrc(pbase + (int64_t)key0 * 8, (uint32_t)left * 8);
     if (lane < 16) buffer_load_lds4_m0(prs, st + L::K_BYTES + L::V_BYTES + wave_pos, p_voff);
   };
 
@@ -250,8 +270,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   float m_use = 0.f;                // m_run * c, or 0 while the row has seen nothing
   float l_run = 0.f;                // this lane's partial row sum
 
-  // mode: 1 every key of the tile visible to every row of the wave, 2 element-masked
-  auto compute = [&](int stage, int t, int mode) {
+  // mode: 1 every key of the tile visible to every row of the wave, 2 element-masked;
+  // left: keys of the tile's block from the tile's first key on
+  auto compute = [&](int stage, int left, int mode) {
     const char* sb = smem + stage * L::STAGE_BYTES;
 
     f32x16 sacc[2];
@@ -278,7 +299,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
       // -1 wraps to the maximum) or k_pos >= 0 (not causal); a padded query row sees
       // nothing when causal
       const char* pl = sb + L::K_BYTES + L::V_BYTES;
-      const int left = p.Sk - t * BN;
       const bool row_sees = p.causal ? (row_ok && qpos >= 0) : row_ok;
       const uint64_t qlim = p.causal ? (uint64_t)qpos : (uint64_t)INT64_MAX;
 #pragma unroll
@@ -371,9 +391,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     for (int r0 = 0; r0 < span; r0 += NTHREADS) {
       const int t = base + r0 + tid;
       bool need = false;
-      int modes = 0;
+      int modes = 0, x = 0;
       if (r0 + tid < span) {
         const TileInfo ti = tinfo[t];
+        int sgi = 0;
+        if constexpr (MULTI)
+          while (sgi + 1 < segs.n && t >= segs.seg[sgi + 1].tile0) ++sgi;
+        x = (sgi << 24) | (t - segs.seg[sgi].tile0);
         need = ti.n_valid > 0 && !(p.causal && qmax_wg < ti.min_valid);
 #pragma unroll
         for (int w = 0; w < NWAVES; ++w) {
@@ -393,37 +417,47 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
       for (int w = 0; w < NWAVES; ++w) tot += wave_cnt[w];
       if (need) tile_list[off + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0))] =
-          make_int2(t, modes);
+          make_int2(x, modes);
       __syncthreads();
       n = tot;
     }
     if (n == 0) continue;
     int issued = 0;
     for (; issued < n && issued < NSTAGE - 1; ++issued)
-      load_tile(__builtin_amdgcn_readfirstlane(tile_list[issued].x), issued % NSTAGE);
+      load_tile(tile_src(__builtin_amdgcn_readfirstlane(tile_list[issued].x)), issued % NSTAGE);
     // list entries of the next step (the tile to compute with this wave's mode, and the
-    // tile to load) are fetched at the end of the previous step, so the step itself does
-    // not wait for LDS latency
+    // buffer sources of the tile to load) are worked out at the end of the previous step, so
+    // the step itself does not wait for LDS or kernel-argument latency
     const int mshift = 2 * wave;
-    auto entry = [&](int i, int& t, int& mode) {
+    auto entry = [&](int i, int& left, int& mode) {
       const int2 e = tile_list[i];
-      t = __builtin_amdgcn_readfirstlane(e.x);
+      const int x = __builtin_amdgcn_readfirstlane(e.x);
+      left = seg_of(x).Sk - (x & 0xffffff) * BN;
       mode = __builtin_amdgcn_readfirstlane((e.y >> mshift) & 3);
     };
-    int t_cur, m_cur;
-    entry(0, t_cur, m_cur);
-    int t_load = issued < n ? __builtin_amdgcn_readfirstlane(tile_list[issued].x) : 0;
+    int left_cur, m_cur;
+    entry(0, left_cur, m_cur);
+    // single block: the sources are a few scalar operations on registers, built at issue time
+    int x_load = issued < n ? __builtin_amdgcn_readfirstlane(tile_list[issued].x) : 0;
+    TileSrc src_load;
+    if constexpr (MULTI) {
+      if (issued < n) src_load = tile_src(x_load);
+    }
     for (int i = 0; i < n; ++i) {
       wait_tiles_ahead<L::LOADS_PER_TILE>(issued - i - 1);
       barrier_no_fence();  // tile i landed for every wave; the stage of tile i-1 is free
       if (issued < n) {
-        load_tile(t_load, issued % NSTAGE);
+        if constexpr (MULTI) load_tile(src_load, issued % NSTAGE);
+        else load_tile(tile_src(x_load), issued % NSTAGE);
         ++issued;
       }
-      if (m_cur != 0) compute(i % NSTAGE, t_cur, m_cur);
+      if (m_cur != 0) compute(i % NSTAGE, left_cur, m_cur);
       if (i + 1 < n) {
-        entry(i + 1, t_cur, m_cur);
-        if (issued < n) t_load = __builtin_amdgcn_readfirstlane(tile_list[issued].x);
+        entry(i + 1, left_cur, m_cur);
+        if (issued < n) {
+          x_load = __builtin_amdgcn_readfirstlane(tile_list[issued].x);
+          if constexpr (MULTI) src_load = tile_src(x_load);
+        }
       }
     }
     __syncthreads();  // the next pass rewrites the list and the stages
@@ -506,17 +540,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   }
 }
 
-template <typename T, int D>
-int launch_typed(const AttnParams& p, hipStream_t st) {
+template <typename T, int D, bool MULTI>
+int launch_typed(const AttnParams& p, const KvSegs& segs, hipStream_t st) {
   const int nqb = (p.Sq + BM - 1) / BM;
   const int64_t total = (int64_t)nqb * p.Hq * p.B;
   if (total == 0) return CEA_OK;
   CEA_REQUIRE(total < (int64_t)1 << 31, CEA_EUNSUPPORTED, "attention: grid too large");
-  const hipError_t e = reserve_lds<attn_prefill_kernel<T, D>>(Layout<D>::LDS_BYTES);
+  const hipError_t e = reserve_lds<attn_prefill_kernel<T, D, MULTI>>(Layout<D>::LDS_BYTES);
   CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "attention: cannot reserve %d bytes of LDS: %s",
               Layout<D>::LDS_BYTES, hipGetErrorString(e));
-  hipLaunchKernelGGL((attn_prefill_kernel<T, D>), dim3((unsigned)total), dim3(NTHREADS),
-                     Layout<D>::LDS_BYTES, st, p);
+  hipLaunchKernelGGL((attn_prefill_kernel<T, D, MULTI>), dim3((unsigned)total), dim3(NTHREADS),
+                     Layout<D>::LDS_BYTES, st, p, segs);
   CEA_CHECK_LAUNCH("attention_prefill");
   return CEA_OK;
 }
@@ -525,7 +559,21 @@ int launch_typed(const AttnParams& p, hipStream_t st) {
 
 static bool al16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
-bool prefill_mfma_supported(const AttnParams& p) {
+KvSegs single_segment(const AttnParams& p) {
+  KvSegs s;
+  memset(&s, 0, sizeof(s));
+  s.n = 1;
+  KvSeg& g = s.seg[0];
+  g.k = p.k; g.v = p.v; g.k_pos = p.k_pos;
+  g.ks_b = p.ks_b; g.ks_h = p.ks_h; g.vs_b = p.vs_b; g.vs_h = p.vs_h;
+  g.kps_b = p.kps_b; g.kps_s = p.kps_s;
+  g.Sk = p.Sk;
+  g.tile0 = 0;
+  return s;
+}
+
+// everything but the KV blocks: dtypes, head size, scale, q / out / final_out layout
+static bool prefill_common_ok(const AttnParams& p) {
   if (!(p.in_dtype == CEA_BF16 || p.in_dtype == CEA_F16)) return false;
   if (!(p.D == 64 || p.D == 128)) return false;
   if (!(p.out_dtype == CEA_F32 || p.out_dtype == p.in_dtype)) return false;
@@ -539,39 +587,76 @@ bool prefill_mfma_supported(const AttnParams& p) {
   // -inf of masked scores into NaN); degenerate scales use the generic kernel
   if (!(fabs(p.scale) >= 1e-30 && fabs(p.scale) <= 1e30)) return false;
   // 16-byte fragments: 8-element aligned strides and bases
-  const int64_t s8[] = {p.qs_b, p.qs_s, p.qs_h, p.ks_b, p.ks_s, p.ks_h, p.vs_b, p.vs_s, p.vs_h};
+  const int64_t s8[] = {p.qs_b, p.qs_s, p.qs_h, p.ks_s, p.vs_s};
   for (int64_t s : s8)
     if (s % 8) return false;
-  if (!al16(p.q) || !al16(p.k) || !al16(p.v) || !al16(p.out)) return false;
+  if (!al16(p.q) || !al16(p.out)) return false;
   const int64_t so[] = {p.os_b, p.os_s, p.os_h};
   for (int64_t s : so)
     if (s % 4) return false;
-  // key positions are fetched 16 bytes at a time: contiguous, 16-byte aligned per batch
-  if (p.kps_s != 1 || p.kps_b % 2 || !al16(p.k_pos)) return false;
   // buffer resources address one (batch, kv head) block with 32-bit offsets: rows must not
-  // overlap and the block must stay below 2 GiB
+  // overlap, and the per-lane row offsets of a tile (up to 63 rows past its first key) must
+  // not wrap 32 bits
   if (p.ks_s < p.D || p.vs_s < p.D) return false;
-  const int64_t kspan = ((int64_t)p.Sk - 1) * p.ks_s * 2 + p.D * 2;
-  const int64_t vspan = ((int64_t)p.Sk - 1) * p.vs_s * 2 + p.D * 2;
-  if (kspan >= ((int64_t)1 << 31) || vspan >= ((int64_t)1 << 31)) return false;
-  // the per-lane row offsets of a tile (up to 63 rows past its first key) must not wrap 32 bits
   if ((int64_t)kTileKeys * p.ks_s * 2 >= ((int64_t)1 << 31) ||
       (int64_t)kTileKeys * p.vs_s * 2 >= ((int64_t)1 << 31))
     return false;
   return true;
 }
 
-int launch_attn_prefill_mfma(const AttnParams& p, hipStream_t st) {
+// one KV block of a launch (row strides p.ks_s / p.vs_s)
+static bool prefill_block_ok(const AttnParams& p, const KvSeg& g) {
+  const int64_t s8[] = {g.ks_b, g.ks_h, g.vs_b, g.vs_h};
+  for (int64_t s : s8)
+    if (s % 8) return false;
+  if (!al16(g.k) || !al16(g.v)) return false;
+  // key positions are fetched 16 bytes at a time: contiguous, 16-byte aligned per batch
+  if (g.kps_s != 1 || g.kps_b % 2 || !al16(g.k_pos)) return false;
+  // the block of one (batch, kv head) stays below 2 GiB
+  const int64_t kspan = ((int64_t)g.Sk - 1) * p.ks_s * 2 + p.D * 2;
+  const int64_t vspan = ((int64_t)g.Sk - 1) * p.vs_s * 2 + p.D * 2;
+  if (kspan >= ((int64_t)1 << 31) || vspan >= ((int64_t)1 << 31)) return false;
+  return true;
+}
+
+bool prefill_mfma_supported(const AttnParams& p) {
+  return prefill_common_ok(p) && prefill_block_ok(p, single_segment(p).seg[0]);
+}
+
+bool prefill_segs_supported(const AttnParams& p, const KvSegs& segs) {
+  if (p.accumulate || p.final_out || !prefill_common_ok(p)) return false;
+  if (segs.n < 1 || segs.n > kMaxKvSegs) return false;
+  int64_t tiles = 0;
+  for (int i = 0; i < segs.n; ++i) {
+    const KvSeg& g = segs.seg[i];
+    if (g.Sk < 1 || g.tile0 != tiles || !prefill_block_ok(p, g)) return false;
+    tiles += (g.Sk + kTileKeys - 1) / kTileKeys;
+  }
+  // list entries hold the block in bits 24.. and its tile in bits 0..23
+  return tiles == p.ntiles && tiles < ((int64_t)1 << 24);
+}
+
+template <bool MULTI>
+static int launch_dispatch(const AttnParams& p, const KvSegs& segs, hipStream_t st) {
   if (p.in_dtype == CEA_BF16) {
-    if (p.D == 128) return launch_typed<bf16, 128>(p, st);
-    if (p.D == 64) return launch_typed<bf16, 64>(p, st);
+    if (p.D == 128) return launch_typed<bf16, 128, MULTI>(p, segs, st);
+    if (p.D == 64) return launch_typed<bf16, 64, MULTI>(p, segs, st);
   } else if (p.in_dtype == CEA_F16) {
-    if (p.D == 128) return launch_typed<f16, 128>(p, st);
-    if (p.D == 64) return launch_typed<f16, 64>(p, st);
+    if (p.D == 128) return launch_typed<f16, 128, MULTI>(p, segs, st);
+    if (p.D == 64) return launch_typed<f16, 64, MULTI>(p, segs, st);
   }
   set_error("attention: MFMA path does not cover dtype %s, head size %d",
             dtype_name(p.in_dtype), p.D);
   return CEA_EUNSUPPORTED;
+}
+
+int launch_attn_prefill_mfma(const AttnParams& p, hipStream_t st) {
+  return launch_dispatch<false>(p, single_segment(p), st);
+}
+
+int launch_attn_prefill_segs(const AttnParams& p, const KvSegs& segs, hipStream_t st) {
+  if (segs.n == 1) return launch_dispatch<false>(p, segs, st);
+  return launch_dispatch<true>(p, segs, st);
 }
 
 }  // namespace cea

@@ -381,6 +381,150 @@ int cea_attention_merge_final(const cea_tensor* q, const cea_tensor* k, const ce
   return merge_impl(1, out, lse, final_out, nullptr, 0, st);
 }
 
+// ---- one rank's share of ring attention with every block resident -----------------------
+// The non-empty blocks, in ring order, become the segment table of one prefill launch when
+// the MFMA kernel covers them (one row stride shared by all blocks); otherwise the blocks run
+// one launch each, merged into running f32/f64 (out, lse) buffers exactly as the reference's
+// per-step merge does.
+struct RingPlan {
+  AttnParams p;   // q / out / lse / head map, row strides of the first non-empty block
+  KvSegs segs;    // non-empty blocks in ring order
+  int first;      // index of the first non-empty block, -1 if every block is empty
+  bool fused;
+  size_t bytes;   // workspace this call needs
+};
+
+static int ring_plan(RingPlan* rp, const cea_tensor* q, int32_t n, const cea_tensor* ks,
+                     const cea_tensor* vs, const cea_tensor* q_pos, const cea_tensor* k_pos_s,
+                     int32_t causal, double scale, const int32_t* kv_map, int32_t kv_map_len,
+                     cea_tensor* out, cea_tensor* lse) {
+  CEA_REQUIRE(n >= 1 && n <= CEA_MAX_PARTS, CEA_EUNSUPPORTED,
+              "ring_attention: between 1 and %d KV blocks per call supported, got %d",
+              CEA_MAX_PARTS, n);
+  CEA_REQUIRE(q && ks && vs && q_pos && k_pos_s && out, CEA_EINVAL, "ring_attention: missing tensor");
+  memset(rp, 0, sizeof(*rp));
+  rp->first = -1;
+  bool same_rows = true;
+  int64_t tiles = 0;
+  size_t block_ws = 0;
+  for (int i = 0; i < n; ++i) {
+    AttnParams bp;
+    int rc = make_attn_params(&bp, q, &ks[i], &vs[i], q_pos, &k_pos_s[i], causal, scale, kv_map,
+                              kv_map_len, out, lse, 0);
+    if (rc) return rc;
+    if (i == 0) rp->p = bp;
+    CEA_REQUIRE(bp.Hkv == rp->p.Hkv, CEA_EINVAL,
+                "ring_attention: block %d has %d KV heads, block 0 has %d", i, bp.Hkv, rp->p.Hkv);
+    const size_t w = cea_attention_workspace_bytes(bp.B, bp.Sq, bp.Hq, bp.Sk, bp.Hkv, bp.D,
+                                                   bp.in_dtype);
+    block_ws = w > block_ws ? w : block_ws;
+    if (bp.Sk == 0) continue;
+    if (rp->first < 0) {
+      rp->first = i;
+      rp->p = bp;
+    } else {
+      same_rows = same_rows && bp.ks_s == rp->p.ks_s && bp.vs_s == rp->p.vs_s;
+    }
+    KvSeg& g = rp->segs.seg[rp->segs.n++];
+    g.k = bp.k; g.v = bp.v; g.k_pos = bp.k_pos;
+    g.ks_b = bp.ks_b; g.ks_h = bp.ks_h; g.vs_b = bp.vs_b; g.vs_h = bp.vs_h;
+    g.kps_b = bp.kps_b; g.kps_s = bp.kps_s;
+    g.Sk = bp.Sk;
+    g.tile0 = (int32_t)tiles;
+    tiles += ntiles_of(bp.Sk);
+  }
+  rp->p.ntiles = (int32_t)tiles;
+  rp->fused = rp->first >= 0 && same_rows && tiles < ((int64_t)1 << 24) &&
+              prefill_segs_supported(rp->p, rp->segs);
+  if (rp->fused) {
+    rp->bytes = tile_bytes(rp->p.B, tiles);
+  } else {
+    // running (out, lse) in the accumulation dtype unless the caller's pair is that already
+    const size_t esz = rp->p.in_dtype == CEA_F64 ? 8 : 4;
+    const size_t run = lse ? 0
+                           : align_up((size_t)rp->p.B * rp->p.Sq * rp->p.Hq * rp->p.D * esz, 256) +
+                                 align_up((size_t)rp->p.B * rp->p.Hq * rp->p.Sq * esz, 256);
+    rp->bytes = run + block_ws;
+  }
+  return CEA_OK;
+}
+
+extern "C" size_t cea_ring_attention_workspace_bytes(const cea_tensor* q, int32_t n,
+                                                     const cea_tensor* ks, const cea_tensor* vs,
+                                                     const cea_tensor* q_pos,
+                                                     const cea_tensor* k_pos_s, int32_t causal,
+                                                     const int32_t* kv_map, int32_t kv_map_len,
+                                                     const cea_tensor* out, const cea_tensor* lse) {
+  RingPlan rp;
+  // scale does not change the route; an invalid call needs no workspace (it fails anyway)
+  if (ring_plan(&rp, q, n, ks, vs, q_pos, k_pos_s, causal, 1.0, kv_map, kv_map_len,
+                (cea_tensor*)out, (cea_tensor*)lse))
+    return 256;
+  return rp.bytes > 256 ? rp.bytes : 256;
+}
+
+extern "C" int cea_ring_attention(const cea_tensor* q, int32_t n, const cea_tensor* ks,
+                                  const cea_tensor* vs, const cea_tensor* q_pos,
+                                  const cea_tensor* k_pos_s, int32_t causal, double scale,
+                                  const int32_t* kv_map, int32_t kv_map_len, cea_tensor* out,
+                                  cea_tensor* lse, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  RingPlan rp;
+  int rc = ring_plan(&rp, q, n, ks, vs, q_pos, k_pos_s, causal, scale, kv_map, kv_map_len, out,
+                     lse);
+  if (rc) return rc;
+  CEA_REQUIRE(workspace != nullptr && workspace_bytes >= rp.bytes, CEA_ENOSPACE,
+              "ring_attention: workspace of %zu bytes needed, %zu given", rp.bytes,
+              workspace_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  if (rp.fused) {
+    rp.p.tiles = (const TileInfo*)workspace;
+    if ((rc = launch_tile_info_segs(rp.segs, rp.p.B, (TileInfo*)workspace, rp.p.ntiles, st)))
+      return rc;
+    return launch_attn_prefill_segs(rp.p, rp.segs, st);
+  }
+  // block after block into the running pair, then the one-partial merge casts it into out
+  char* ws = (char*)workspace;
+  size_t left = workspace_bytes;
+  cea_tensor run_out = *out, run_lse;
+  if (lse) {
+    run_lse = *lse;
+  } else {
+    const int acc = rp.p.in_dtype == CEA_F64 ? CEA_F64 : CEA_F32;
+    const int64_t esz = acc == CEA_F64 ? 8 : 4;
+    const int64_t B = rp.p.B, Sq = rp.p.Sq, Hq = rp.p.Hq, D = rp.p.D;
+    memset(&run_out, 0, sizeof(run_out));
+    run_out.data = ws;
+    run_out.dtype = acc;
+    run_out.ndim = 4;
+    const int64_t osz[4] = {B, Sq, Hq, D}, ost[4] = {Sq * Hq * D, Hq * D, D, 1};
+    for (int j = 0; j < 4; ++j) { run_out.size[j] = osz[j]; run_out.stride[j] = ost[j]; }
+    const size_t ob = align_up((size_t)(B * Sq * Hq * D * esz), 256);
+    memset(&run_lse, 0, sizeof(run_lse));
+    run_lse.data = ws + ob;
+    run_lse.dtype = acc;
+    run_lse.ndim = 3;
+    const int64_t lsz[3] = {B, Hq, Sq}, lst[3] = {Hq * Sq, Sq, 1};
+    for (int j = 0; j < 3; ++j) { run_lse.size[j] = lsz[j]; run_lse.stride[j] = lst[j]; }
+    const size_t used = ob + align_up((size_t)(B * Hq * Sq * esz), 256);
+    ws += used;
+    left -= used;
+  }
+  int done = 0;
+  for (int i = 0; i < n; ++i) {
+    // every block empty: the first one writes the merge's neutral element (0, -inf)
+    if (ks[i].size[1] == 0 && !(rp.first < 0 && i == 0)) continue;
+    AttnParams bp;
+    if ((rc = make_attn_params(&bp, q, &ks[i], &vs[i], q_pos, &k_pos_s[i], causal, scale, kv_map,
+                               kv_map_len, &run_out, &run_lse, done > 0 ? 1 : 0)))
+      return rc;
+    if ((rc = run_attention(bp, ws, left, st))) return rc;
+    ++done;
+  }
+  if (lse) return CEA_OK;
+  return merge_impl(1, &run_out, &run_lse, out, nullptr, 0, st);
+}
+
 static int fill_merge_part(MergeParams* m, int i, const cea_tensor* o, const cea_tensor* l,
                            int64_t B, int64_t Sq, int64_t H, int64_t D, int dt) {
   int rc;

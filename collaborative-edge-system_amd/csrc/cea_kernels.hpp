@@ -37,6 +37,24 @@ struct AttnParams {
   int32_t final_dtype;
 };
 
+// KV blocks of one prefill launch, in the order their tiles are visited (a ring share's
+// blocks in ring order; one block for an ordinary call).  Row strides (ks_s / vs_s) are the
+// launch's AttnParams ones, shared by every block; tile0 is the block's first tile in the
+// launch's tile numbering (and in its tile-summary array).
+constexpr int kMaxKvSegs = CEA_MAX_PARTS;
+struct KvSeg {
+  const void* k;
+  const void* v;
+  const int64_t* k_pos;
+  int64_t ks_b, ks_h, vs_b, vs_h, kps_b, kps_s;
+  int32_t Sk;
+  int32_t tile0;
+};
+struct KvSegs {
+  int32_t n;
+  KvSeg seg[kMaxKvSegs];
+};
+
 // n-way merge of partial results (n <= CEA_MAX_PARTS).
 struct MergeParams {
   int32_t n;
@@ -166,8 +184,17 @@ int launch_linear(const cea_tensor* x, const cea_tensor* wg, const cea_tensor* w
 int launch_attn_generic(const AttnParams& p, hipStream_t s);
 int launch_tile_info(const int64_t* k_pos, int64_t kps_b, int64_t kps_s, int32_t B, int32_t Sk,
                      TileInfo* tiles, int32_t ntiles, hipStream_t s);
+// summaries of every block of 'segs' into one [B, ntiles] array (ntiles = all blocks' tiles)
+int launch_tile_info_segs(const KvSegs& segs, int32_t B, TileInfo* tiles, int32_t ntiles,
+                          hipStream_t s);
+// the KV block of p as a one-entry segment table
+KvSegs single_segment(const AttnParams& p);
 bool prefill_mfma_supported(const AttnParams& p);
+// p carries q / out / lse / head map / row strides; the blocks come from segs (p.k, p.v,
+// p.k_pos and p.Sk are not read); p.ntiles and p.tiles cover all blocks
+bool prefill_segs_supported(const AttnParams& p, const KvSegs& segs);
 int launch_attn_prefill_mfma(const AttnParams& p, hipStream_t s);
+int launch_attn_prefill_segs(const AttnParams& p, const KvSegs& segs, hipStream_t s);
 bool f32_mfma_supported(const AttnParams& p);
 int launch_attn_f32_mfma(const AttnParams& p, hipStream_t s);
 bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype,

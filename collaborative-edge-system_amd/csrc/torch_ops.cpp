@@ -90,18 +90,33 @@ void* stream_of(const at::Device& d) {
 // The kernels' workspace: one buffer per (device, stream), grown to the largest request seen
 // and then reused by every call on that stream (calls on one stream run in order, so a call
 // never overwrites scratch a queued call still reads).  A grown-out buffer returns to
-// PyTorch's caching allocator, which hands its memory out again only in stream order.
+// PyTorch's caching allocator, which hands its memory out again only in stream order - unless
+// a HIP graph capture may have recorded it: graph replays keep writing to the captured
+// address whatever the allocator has since handed it to, so such a buffer is kept alive
+// (retired, never freed) when a larger one replaces it.
+struct WsEntry {
+  Tensor t;
+  bool captured = false;  // used while its stream was capturing a graph
+};
 std::mutex g_ws_mu;
-std::map<std::pair<int, void*>, Tensor> g_ws;
+std::map<std::pair<int, void*>, WsEntry> g_ws;
+std::vector<Tensor> g_ws_retired;
 
 Tensor workspace(size_t bytes, const at::Device& d) {
   void* st = stream_of(d);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const bool capturing =
+      hipStreamIsCapturing((hipStream_t)st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
   const int64_t want = (int64_t)std::max<size_t>((bytes + 4095) & ~(size_t)4095, 4096);
   std::lock_guard<std::mutex> lock(g_ws_mu);
-  Tensor& t = g_ws[{(int)d.index(), st}];
-  if (!t.defined() || t.numel() < want)
-    t = at::empty({want}, at::TensorOptions().dtype(at::kByte).device(d));
-  return t;
+  WsEntry& e = g_ws[{(int)d.index(), st}];
+  if (!e.t.defined() || e.t.numel() < want) {
+    if (e.t.defined() && (e.captured || capturing)) g_ws_retired.push_back(e.t);
+    e.t = at::empty({want}, at::TensorOptions().dtype(at::kByte).device(d));
+    e.captured = false;
+  }
+  e.captured = e.captured || capturing;
+  return e.t;
 }
 
 // q / k / v style operands need a unit innermost stride
@@ -252,6 +267,46 @@ std::vector<Tensor> partitioned(const Tensor& q_in, const Tensor& q_pos_in, at::
     res.push_back(plses[i]);
   }
   return res;
+}
+
+// One rank's share of ring attention over KV blocks in ring order (cea_ring_attention).
+std::vector<Tensor> ring(const Tensor& q_in, const Tensor& q_pos_in, at::TensorList ks_in,
+                         at::TensorList vs_in, at::TensorList ps_in, bool causal, double scale,
+                         c10::optional<at::IntArrayRef> kv_map, bool with_lse) {
+  const int64_t n = (int64_t)ks_in.size();
+  TORCH_CHECK_VALUE(n >= 1 && (int64_t)vs_in.size() == n && (int64_t)ps_in.size() == n,
+                    "need one k, v and position tensor per KV block");
+  const at::Device dev = device_of({&q_in, &q_pos_in}, ks_in);
+  device_of({}, vs_in);
+  device_of({}, ps_in);
+  const Tensor q = inner(q_in), qp = as_i64(q_pos_in);
+  TORCH_CHECK_VALUE(q.dim() == 4, "q must be [B, S, H, D]");
+  std::vector<Tensor> ks, vs, ps;
+  for (int64_t i = 0; i < n; ++i) {
+    ks.push_back(inner(ks_in[i]));
+    vs.push_back(inner(vs_in[i]));
+    ps.push_back(as_i64(ps_in[i]));
+  }
+  const int64_t B = q.size(0), Sq = q.size(1), Hq = q.size(2), D = q.size(3);
+  const at::ScalarType acc = acc_of(q.scalar_type());
+  const auto opts = q.options();
+  Tensor out = at::empty({B, Sq, Hq, D}, opts.dtype(with_lse ? acc : q.scalar_type()));
+  Tensor lse = with_lse ? at::empty({B, Hq, Sq}, opts.dtype(acc)) : Tensor();
+  c10::DeviceGuard guard(dev);
+  const std::vector<int32_t> m = map_of(kv_map);
+  cea_tensor qa = arg(q), qpa = arg(qp), o = arg(out);
+  cea_tensor l = with_lse ? arg(lse) : cea_tensor{};
+  std::vector<cea_tensor> ka = args(ks), va = args(vs), pa = args(ps);
+  const size_t ws_bytes = cea_ring_attention_workspace_bytes(
+      &qa, (int32_t)n, ka.data(), va.data(), &qpa, pa.data(), causal ? 1 : 0,
+      m.empty() ? nullptr : m.data(), (int32_t)m.size(), &o, with_lse ? &l : nullptr);
+  Tensor ws = workspace(ws_bytes, dev);
+  check_rc(cea_ring_attention(&qa, (int32_t)n, ka.data(), va.data(), &qpa, pa.data(), causal ? 1 : 0, scale,
+                              m.empty() ? nullptr : m.data(), (int32_t)m.size(), &o,
+                              with_lse ? &l : nullptr, ws.data_ptr(), (size_t)ws.numel(), stream_of(dev)),
+           "ring_attention");
+  if (with_lse) return {out, lse};
+  return {out};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -479,6 +534,8 @@ TORCH_LIBRARY(collab_edge, m) {
   m.def("merge(Tensor[] outs, Tensor[] lses, bool pairwise, ScalarType? out_dtype) -> Tensor[]");
   m.def("partitioned(Tensor q, Tensor q_pos, Tensor[] ks, Tensor[] vs, Tensor[] ps, bool causal, "
         "float scale, int[]? kv_map, ScalarType out_dtype, bool with_lse, bool with_parts) -> Tensor[]");
+  m.def("ring(Tensor q, Tensor q_pos, Tensor[] ks, Tensor[] vs, Tensor[] ps, bool causal, float scale, "
+        "int[]? kv_map, bool with_lse) -> Tensor[]");
   m.def("pack_partial(Tensor out, Tensor lse, Tensor(a!) packed) -> ()");
   m.def("merge_packed(Tensor[] parts, ScalarType out_dtype, bool with_lse) -> Tensor[]");
   m.def("ulysses_scatter(Tensor[] qs, Tensor[] ks, Tensor[] vs, Tensor[] ps, int q_start, int q_count, "
@@ -502,6 +559,7 @@ TORCH_LIBRARY_IMPL(collab_edge, CompositeExplicitAutograd, m) {
   m.impl("attention_into", attention_into);
   m.impl("merge", merge);
   m.impl("partitioned", partitioned);
+  m.impl("ring", ring);
   m.impl("pack_partial", pack_partial);
   m.impl("merge_packed", merge_packed);
   m.impl("ulysses_scatter", ulysses_scatter);

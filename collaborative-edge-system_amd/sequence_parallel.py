@@ -130,6 +130,61 @@ def _raw_kv(comm: LocalGroup, src: int):
 # --------------------------------------------------------------------------------------
 # ring attention
 # --------------------------------------------------------------------------------------
+def _ring_pieces(k, v, k_pos, comm: LocalGroup, kv_sizes: Sequence[int], kv_block: Optional[int]):
+    """The KV pieces rank ``comm.rank`` attends to, in ring order: the block of rank
+    ``(r - step) mod n`` at step ``step`` (sequence_parallel.py:107-127), as the ring delivers
+    it, split into ``kv_block``-key pieces when ``kv_block`` is given (attention.py:225-236)."""
+    n, r = comm.size, comm.rank
+    if kv_block is not None and kv_block < 1:
+        raise ValueError("kv_block must be positive")
+    if len(kv_sizes) != n or kv_sizes[r] != k.shape[1]:
+        raise ValueError(f"kv_sizes {list(kv_sizes)} inconsistent with local block of {k.shape[1]} tokens")
+    own = (k, v, k_pos)
+    pieces = []
+    for step in range(n):
+        src = (r - step) % n
+        kb, vb, pb = _kv_from(comm, src, own)
+        if kb.shape[1] != kv_sizes[src]:
+            raise ValueError(f"kv_sizes {list(kv_sizes)} inconsistent with the block of rank {src}")
+        size = kb.shape[1]
+        blk = kv_block if kv_block is not None and kv_block < size else max(size, 1)
+        for start in range(0, size, blk):
+            end = min(start + blk, size)
+            pieces.append((kb[:, start:end], vb[:, start:end], pb[:, start:end]))
+    return pieces
+
+
+def _ring(q, k, v, q_pos, k_pos, comm, kv_sizes, causal, scale, kv_map, kv_block, with_lse):
+    pieces = _ring_pieces(k, v, k_pos, comm, kv_sizes, kv_block)
+    acc = accumulation_dtype(q.dtype)
+    if not pieces:  # no rank held a key: the merge's neutral element
+        out = torch.zeros(q.shape, dtype=acc if with_lse else q.dtype, device=q.device)
+        lse = torch.full((q.shape[0], q.shape[2], q.shape[1]), float("-inf"), dtype=acc,
+                         device=q.device)
+        return (out, lse) if with_lse else out
+    mapping = _kv_map_list(kv_map)
+    for kb, vb, _ in pieces:
+        _check_heads(q.shape[2], kb.shape[2], mapping)
+        if kb.dtype != q.dtype or vb.dtype != q.dtype:
+            raise ValueError(f"q, k and v must share a dtype, got {q.dtype}, {kb.dtype}, {vb.dtype}")
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
+    if len(pieces) <= nat.MAX_PARTS:
+        # every piece in one call (cea_ring_attention): one launch for the MFMA kernel
+        res = nat.ops().ring(q, q_pos, [x[0] for x in pieces], [x[1] for x in pieces],
+                             [x[2] for x in pieces], bool(causal), scale, mapping, bool(with_lse))
+        return (res[0], res[1]) if with_lse else res[0]
+    # more pieces than one call takes: piece after piece, merged in the kernel epilogue
+    B, Sq, Hq, D = q.shape
+    out = torch.empty(B, Sq, Hq, D, dtype=acc, device=q.device)
+    lse = torch.empty((B, Hq, Sq), dtype=acc, device=q.device)
+    final = None if with_lse else torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    for i, (kb, vb, pb) in enumerate(pieces):
+        last = i == len(pieces) - 1
+        attention_with_lse_into(out, lse, q, kb, vb, q_pos, pb, causal=causal, scale=scale,
+                                kv_map=kv_map, accumulate=i > 0, final=final if last else None)
+    return (out, lse) if with_lse else final
+
+
 def ring_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -145,13 +200,18 @@ def ring_attention(
     kv_block: Optional[int] = None,
 ) -> torch.Tensor:
     """Attention of this rank's queries over the KV blocks of all ranks
-    (sequence_parallel.py:68-130); returns ``[B, s_r, Hq, D]`` in ``q.dtype``.  The last
-    block's merge writes the result in ``q.dtype`` directly (the reference's final
-    ``out.to(q.dtype)``, :128, in the same kernel)."""
-    final = torch.empty(q.shape, dtype=q.dtype, device=q.device) if comm.size > 1 else None
-    out, _ = ring_attention_with_lse(q, k, v, q_pos, k_pos, comm, kv_sizes, causal=causal,
-                                     scale=scale, kv_map=kv_map, kv_block=kv_block, _final=final)
-    return final if final is not None else out.to(q.dtype)
+    (sequence_parallel.py:68-130); returns ``[B, s_r, Hq, D]`` in ``q.dtype``.
+
+    Every block is resident here, so the rank's whole share is one call: its blocks in ring
+    order form one kernel launch that carries each query row's softmax state from block to
+    block and writes the result in ``q.dtype`` once (the reference's per-step merge and final
+    ``out.to(q.dtype)``, :121 and :128).  Blocks no query can see cost one pass over their
+    position summaries, which replaces the reference's ``fully_masked`` skip (:117)."""
+    if comm.size == 1:
+        out, _ = attention_with_lse(q, k, v, q_pos, k_pos, causal=causal, scale=scale,
+                                    kv_map=kv_map, kv_block=kv_block)
+        return out.to(q.dtype)
+    return _ring(q, k, v, q_pos, k_pos, comm, kv_sizes, causal, scale, kv_map, kv_block, False)
 
 
 def ring_attention_with_lse(
@@ -167,49 +227,12 @@ def ring_attention_with_lse(
     scale: Optional[float] = None,
     kv_map: KVMap = None,
     kv_block: Optional[int] = None,
-    _final: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """:func:`ring_attention` returning the merged ``(out, lse)`` in accumulation precision
-    (``_final``: a tensor that receives the merged output of the last merge instead; ``out``
-    is then unspecified)."""
-    n, r = comm.size, comm.rank
-    if kv_block is not None and kv_block < 1:
-        raise ValueError("kv_block must be positive")
-    if n == 1:
+    """:func:`ring_attention` returning the merged ``(out, lse)`` in accumulation precision."""
+    if comm.size == 1:
         return attention_with_lse(q, k, v, q_pos, k_pos, causal=causal, scale=scale,
                                   kv_map=kv_map, kv_block=kv_block)
-    if len(kv_sizes) != n or kv_sizes[r] != k.shape[1]:
-        raise ValueError(f"kv_sizes {list(kv_sizes)} inconsistent with local block of {k.shape[1]} tokens")
-    B, Sq, Hq, D = q.shape
-    acc = accumulation_dtype(q.dtype)
-    # the first non-empty block writes (out, lse); later ones merge into them in the kernel
-    out = torch.empty(B, Sq, Hq, D, dtype=acc, device=q.device)
-    lse = torch.empty((B, Hq, Sq), dtype=acc, device=q.device)
-    own = (k, v, k_pos)
-    launches = []
-    for step in range(n):
-        kb, vb, pb = _kv_from(comm, (r - step) % n, own)
-        if kb.shape[1] != kv_sizes[(r - step) % n]:
-            raise ValueError(f"kv_sizes {list(kv_sizes)} inconsistent with the block of rank {(r - step) % n}")
-        blk = kv_block if kv_block is not None and kv_block < kb.shape[1] else kb.shape[1]
-        for start in range(0, kb.shape[1], blk):
-            end = min(start + blk, kb.shape[1])
-            launches.append((kb[:, start:end], vb[:, start:end], pb[:, start:end]))
-    if not launches:  # no rank held a key: the merge's neutral element
-        out.zero_()
-        lse.fill_(float("-inf"))
-        if _final is not None:
-            _final.zero_()
-        return out, lse
-    for i, (kb, vb, pb) in enumerate(launches):
-        last = i == len(launches) - 1
-        attention_with_lse_into(out, lse, q, kb, vb, q_pos, pb, causal=causal, scale=scale,
-                                kv_map=kv_map, accumulate=i > 0,
-                                final=_final if last and i > 0 else None)
-    if _final is not None and len(launches) == 1:  # a one-partial merge casts it
-        cast, _ = _merge_list([out], [lse], out_dtype=_final.dtype)
-        _final.copy_(cast)
-    return out, lse
+    return _ring(q, k, v, q_pos, k_pos, comm, kv_sizes, causal, scale, kv_map, kv_block, True)
 
 
 # --------------------------------------------------------------------------------------

@@ -132,6 +132,33 @@ int cea_attention_merge_final(const cea_tensor* q, const cea_tensor* k, const ce
                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One rank's share of ring attention when every rank's KV block is resident on this device:
+ * attention of q over n KV blocks given in ring order, merged exactly - what the per-rank
+ * loop of ring_attention returns (collab_infer/parallel/sequence_parallel.py:68-130: the
+ * attention_with_lse of each block :118-120, the online merge_attention :121, the skip of
+ * fully masked blocks :117 and the final out.to(q.dtype) :128).  For bf16 / f16 with head
+ * size 64 or 128 and one row stride shared by the blocks, all blocks run in one launch that
+ * keeps each query row's softmax state across them (one output write, no intermediate
+ * merges); other calls run block after block into a running (out, lse) pair in the
+ * accumulation dtype.  Rows that see no key of any block get out = 0, lse = -inf.
+ *   ks, vs    n tensors [B,Sk_i,Hkv,D], q's dtype, innermost stride 1 (Sk_i may be 0)
+ *   k_pos_s   n tensors [B,Sk_i] i64
+ *   out       [B,Sq,Hq,D] in q's dtype (the reference's return value) or the accumulation
+ *             dtype; with lse it must be the accumulation dtype
+ *   lse       [B,Hq,Sq] accumulation dtype, or NULL
+ *   workspace at least cea_ring_attention_workspace_bytes() of these same arguments
+ */
+size_t cea_ring_attention_workspace_bytes(const cea_tensor* q, int32_t n, const cea_tensor* ks,
+                                          const cea_tensor* vs, const cea_tensor* q_pos,
+                                          const cea_tensor* k_pos_s, int32_t causal,
+                                          const int32_t* kv_map, int32_t kv_map_len,
+                                          const cea_tensor* out, const cea_tensor* lse);
+int cea_ring_attention(const cea_tensor* q, int32_t n, const cea_tensor* ks, const cea_tensor* vs,
+                       const cea_tensor* q_pos, const cea_tensor* k_pos_s, int32_t causal,
+                       double scale, const int32_t* kv_map, int32_t kv_map_len, cea_tensor* out,
+                       cea_tensor* lse, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Pairwise exact merge: lse = logaddexp(lse_a, lse_b); out = out_a*w_a + out_b*w_b.
  * Replaces merge_attention (collab_infer/parallel/attention.py:242-250).
  *   out_*  [B,Sq,H,D] f32/f64,  lse_* [B,H,Sq] same dtype.  out may alias out_a (each
