@@ -74,7 +74,8 @@ template <int D> struct Layout {
   static constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;
   static constexpr int KV_LOADS = K_BYTES / (NTHREADS * 16);  // per wave, for K and for V
   static constexpr int ROWS_PER_LOAD = 1024 / KROW;           // rows one wave load covers
-  static constexpr int LOADS_PER_TILE = 2 * KV_LOADS + 1;     // K, V, positions
+  static constexpr int LOADS_PER_TILE = 2 * KV_LOADS;         // K and V loads of one wave
+  // wave 0 also loads the tile's 64 key positions (512 B, 32 lanes x 16 B) in one load
   static_assert(KV_LOADS >= 1, "tile too small for one load per wave");
 };
 
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     const int lgv = (((pg >> 2) ^ v_swz<D>(key)) << 2) | (pg & 3);
     v_voff[i] = key * vrow_bytes + (lgv << 4);
   }
-  const uint32_t p_voff = wave * 64 + (lane & 15) * 4;  // 8 positions per wave, 16 lanes x 4 B
+  const uint32_t p_voff = (lane & 31) * 16;  // wave 0: 2 positions per lane, lanes 0-31
 
   // fragment reads: K rows for S^T, transposing reads for V^T
   uint32_t k_raddr[D / 16];
@@ -229,11 +230,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   // stage (wave-uniform: scalar registers)
   const uint32_t smem_lds = lds_addr(smem);
   const uint32_t wave_kv = __builtin_amdgcn_readfirstlane(wave) * (L::KV_LOADS * 1024);
-  const uint32_t wave_pos = __builtin_amdgcn_readfirstlane(wave) * 64;
+  const bool pos_loader = __builtin_amdgcn_readfirstlane(wave) == 0;
   // block of a list entry (block << 24 | tile): a compile-time 0 for single-block launches
   auto seg_of = [&](int x) -> const KvSeg& { return segs.seg[MULTI ? (x >> 24) : 0]; };
-  // buffer sources of one tile, worked out a step before its loads are issued (the block's
-  // pointers come from kernel arguments; for several blocks that is a dependent scalar load)
+  // buffer sources of one tile (the block's pointers come from kernel arguments)
   struct TileSrc {
     i32x4 krs, vrs, prs;
   };
@@ -250,15 +250,15 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     ts.prs = make_rsrc(pbase + (int64_t)key0 * 8, (uint32_t)left * 8);
     return ts;
   };
+  // this wave's share of a tile's loads: K rows, V rows and (16 lanes) key positions
   auto load_tile = [&](const TileSrc& ts, int stage) {
-    const i32x4 krs = ts.krs, vrs = ts.vrs, prs = ts.prs;
     const uint32_t st = smem_lds + stage * L::STAGE_BYTES;
 #pragma unroll
-    for (int i = 0; i < L::KV_LOADS; ++i) buffer_load_lds16_m0(krs, st + wave_kv + i * 1024, k_voff[i]);
+    for (int i = 0; i < L::KV_LOADS; ++i) buffer_load_lds16_m0(ts.krs, st + wave_kv + i * 1024, k_voff[i]);
 #pragma unroll
     for (int i = 0; i < L::KV_LOADS; ++i)
-      buffer_load_lds16_m0(vrs, st + L::K_BYTES + wave_kv + i * 1024, v_voff[i]);
-    if (lane < 16) buffer_load_lds4_m0(prs, st + L::K_BYTES + L::V_BYTES + wave_pos, p_voff);
+      buffer_load_lds16_m0(ts.vrs, st + L::K_BYTES + wave_kv + i * 1024, v_voff[i]);
+    if (pos_loader && lane < 32) buffer_load_lds16_m0(ts.prs, st + L::K_BYTES + L::V_BYTES, p_voff);
   };
 
   f32x16 oacc[D / 32];
@@ -425,40 +425,29 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     int issued = 0;
     for (; issued < n && issued < NSTAGE - 1; ++issued)
       load_tile(tile_src(__builtin_amdgcn_readfirstlane(tile_list[issued].x)), issued % NSTAGE);
-    // list entries of the next step (the tile to compute with this wave's mode, and the
-    // buffer sources of the tile to load) are worked out at the end of the previous step, so
-    // the step itself does not wait for LDS or kernel-argument latency
+    // The list entries of the next step (its tile and this wave's mode, and the tile to load
+    // after it) are read from LDS right after the barrier and only used after this step's
+    // work, so their latency hides under it; so does the kernel-argument read of the tile's
+    // block size that masked tiles use.
     const int mshift = 2 * wave;
-    auto entry = [&](int i, int& left, int& mode) {
-      const int2 e = tile_list[i];
-      const int x = __builtin_amdgcn_readfirstlane(e.x);
-      left = seg_of(x).Sk - (x & 0xffffff) * BN;
-      mode = __builtin_amdgcn_readfirstlane((e.y >> mshift) & 3);
-    };
-    int left_cur, m_cur;
-    entry(0, left_cur, m_cur);
-    // single block: the sources are a few scalar operations on registers, built at issue time
+    int x_cur = __builtin_amdgcn_readfirstlane(tile_list[0].x);
+    int m_cur = __builtin_amdgcn_readfirstlane((tile_list[0].y >> mshift) & 3);
     int x_load = issued < n ? __builtin_amdgcn_readfirstlane(tile_list[issued].x) : 0;
-    TileSrc src_load;
-    if constexpr (MULTI) {
-      if (issued < n) src_load = tile_src(x_load);
-    }
     for (int i = 0; i < n; ++i) {
-      wait_tiles_ahead<L::LOADS_PER_TILE>(issued - i - 1);
+      if (pos_loader) wait_tiles_ahead<L::LOADS_PER_TILE + 1>(issued - i - 1);
+      else wait_tiles_ahead<L::LOADS_PER_TILE>(issued - i - 1);
       barrier_no_fence();  // tile i landed for every wave; the stage of tile i-1 is free
       if (issued < n) {
-        if constexpr (MULTI) load_tile(src_load, issued % NSTAGE);
-        else load_tile(tile_src(x_load), issued % NSTAGE);
+        load_tile(tile_src(x_load), issued % NSTAGE);
         ++issued;
       }
+      const int left_cur = seg_of(x_cur).Sk - (x_cur & 0xffffff) * BN;
+      const int2 e_nxt = tile_list[i + 1 < n ? i + 1 : i];
+      const int xl_nxt = tile_list[issued < n ? issued : 0].x;
       if (m_cur != 0) compute(i % NSTAGE, left_cur, m_cur);
-      if (i + 1 < n) {
-        entry(i + 1, left_cur, m_cur);
-        if (issued < n) {
-          x_load = __builtin_amdgcn_readfirstlane(tile_list[issued].x);
-          if constexpr (MULTI) src_load = tile_src(x_load);
-        }
-      }
+      x_cur = __builtin_amdgcn_readfirstlane(e_nxt.x);
+      m_cur = __builtin_amdgcn_readfirstlane((e_nxt.y >> mshift) & 3);
+      x_load = __builtin_amdgcn_readfirstlane(xl_nxt);
     }
     __syncthreads();  // the next pass rewrites the list and the stages
   }
