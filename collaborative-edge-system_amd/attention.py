@@ -271,7 +271,7 @@ def merge_packed(gathered, out_dtype: Optional[torch.dtype] = None, return_lse: 
     parts = list(gathered.unbind(0)) if isinstance(gathered, torch.Tensor) else list(gathered)
     if not parts:
         raise ValueError("need at least one packed partial")
-    if len(parts) > nat.MAX_PARTS:  # merge is associative: reduce in groups, then repack
+    while len(parts) > nat.MAX_PARTS:  # merge is associative: reduce in groups, then repack
         groups = [merge_packed(parts[i : i + nat.MAX_PARTS], return_lse=True)
                   for i in range(0, len(parts), nat.MAX_PARTS)]
         parts = [pack_partial(o, l) for o, l in groups]

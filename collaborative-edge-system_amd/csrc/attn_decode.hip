@@ -204,28 +204,30 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   __shared__ float red_l[NW][NR];
 
   // 1-D grid: pair items of rows [0, pair_rows), then single-chunk items of the other rows;
-  // item fastest, then kv head, then batch row
+  // item fastest, then unit, then batch row - except per-head units, which go fastest so that
+  // the units reading one KV head's chunk run side by side and share its reads in the caches
   const int total_chunks = p.chunk_begin[p.nparts];
-  int b, kvh, item;
+  int b, unit, item;
   {
     const int n2 = p.item_begin[p.nparts];
-    const int first = p.pair_rows * p.Hkv * n2;
+    const int first = p.pair_rows * p.units * n2;
     const int id = blockIdx.x;
-    if (id < first) {
-      b = id / (p.Hkv * n2);
-      kvh = (id / n2) % p.Hkv;
-      item = id % n2;
+    const int r = id < first ? id : id - first;
+    const int ni = id < first ? n2 : total_chunks;  // items per (row, unit)
+    b = (id < first ? 0 : p.pair_rows) + r / (p.units * ni);
+    if (p.per_head) {
+      unit = r % p.units;
+      item = (r / p.units) % ni;
     } else {
-      const int r = id - first;
-      b = p.pair_rows + r / (p.Hkv * total_chunks);
-      kvh = (r / total_chunks) % p.Hkv;
-      item = r % total_chunks;
+      unit = (r / ni) % p.units;
+      item = r % ni;
     }
   }
+  const int kvh = p.per_head ? (int)p.map.kv[unit] : unit;  // KV head the unit reads
   const DecodeItem it = item_of(p, b, item);
   const int part = it.part, chunk = it.chunk, nch = it.nch;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  float* part_out = p.partial + (((int64_t)b * p.Hkv + kvh) * total_chunks + item) * NR * (D + 2);
+  float* part_out = p.partial + (((int64_t)b * p.units + unit) * total_chunks + item) * NR * (D + 2);
   const int row = lane & 15;   // query row (MFMA column) of this lane
   const int grp = lane >> 4;   // 4-key group of the 16-key tile
   const int G = p.G;
@@ -237,15 +239,16 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   // buffer (free until the first tile load), in flight together with the chunk's tile mask, so
   // the workgroup starts streaming after one memory round trip
   {
-    constexpr int QLOADS = NR * D * 2 <= 1024 ? 1 : NR * D * 2 / 1024;
+    constexpr int QROWS = 1024 / L::ROW;  // query rows one 1 KB load covers
+    constexpr int QLOADS = NR <= QROWS ? 1 : NR / QROWS;
     const i32x4 qrs = make_rsrc((const T*)p.q + b * p.qs_b,
                                 (uint32_t)((((int64_t)p.Sq - 1) * p.qs_s + ((int64_t)p.Hq - 1) * p.qs_h + D) * sizeof(T)));
 #pragma unroll
     for (int i = 0; i < QLOADS; ++i) {
-      const int r = i * 4 + (lane >> 4);
+      const int r = i * QROWS + lane / (L::ROW / 16);
       const int rr = r < p.Sq * G ? r : 0;  // padding rows read row 0 (zeroed below)
-      const uint32_t off = (uint32_t)(((int64_t)(rr / G) * p.qs_s + (int64_t)(kvh * G + rr % G) * p.qs_h) * sizeof(T)) +
-                           (lane & 15) * 16;
+      const uint32_t off = (uint32_t)(((int64_t)(rr / G) * p.qs_s + (int64_t)(unit * G + rr % G) * p.qs_h) * sizeof(T)) +
+                           (lane % (L::ROW / 16)) * 16;
       buffer_load_lds16(qrs, wb + i * 1024, off);
     }
   }
@@ -286,19 +289,20 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   for (int i = 0; i < L::LOADS; ++i) {
     const int r = i * (1024 / L::ROW) + lane / (L::ROW / 16);
     const int pg = lane % (L::ROW / 16);                   // physical 16-byte group
-    k_voff[i] = r * krow + ((pg ^ (r & 15)) << 4);          // K: 16-byte groups ^ row
-    const int lgv = ((((pg >> 1) ^ (r & 7)) << 1) | (pg & 1));  // V: 32-byte blocks ^ row
+    k_voff[i] = r * krow + ((pg ^ (r & (L::ROW / 16 - 1))) << 4);          // K: 16-byte groups ^ row
+    const int lgv = ((((pg >> 1) ^ (r & (L::ROW / 32 - 1))) << 1) | (pg & 1));  // V: 32-byte blocks ^ row
     v_voff[i] = r * vrow + (lgv << 4);
   }
   uint32_t k_raddr[D / 32];  // A operand of S: key 'row', features grp*8 + 32*ks
 #pragma unroll
-  for (int ks = 0; ks < D / 32; ++ks) k_raddr[ks] = row * L::ROW + (((grp + 4 * ks) ^ (row & 15)) << 4);
+  for (int ks = 0; ks < D / 32; ++ks)
+    k_raddr[ks] = row * L::ROW + (((grp + 4 * ks) ^ (row & (L::ROW / 16 - 1))) << 4);
   uint32_t v_raddr[D / 16];  // transposing reads: source lane s of group grp -> key grp*4 + s/4
   {
     const int vr = grp * 4 + (row >> 2);
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt)
-      v_raddr[dt] = L::TILE_BYTES + vr * L::ROW + ((dt ^ (vr & 7)) << 5) + 8 * (row & 3);
+      v_raddr[dt] = L::TILE_BYTES + vr * L::ROW + ((dt ^ (vr & (L::ROW / 32 - 1))) << 5) + 8 * (row & 3);
   }
 
   // this wave's tiles: wave, wave + NW, ... that hold a visible key (tile t of the item is
@@ -469,33 +473,54 @@ constexpr int RWAVES = RTHREADS / 64;
 constexpr int RCH = kDecodeMaxChunks;  // chunks staged per row
 constexpr int RPF = 12;                // chunk outputs per wave read ahead of their weights
 
+// Output features per lane: D / 64 consecutive floats (a float2 for D = 128, one float for 64).
+template <int D> struct RVec;
+template <> struct RVec<128> {
+  typedef float2 V;
+  static __device__ __forceinline__ V load(const float* q) { return *(const float2*)q; }
+  static __device__ __forceinline__ V fma(V a, float w, V c) {
+    return V{__builtin_fmaf(a.x, w, c.x), __builtin_fmaf(a.y, w, c.y)};
+  }
+  static __device__ __forceinline__ V add(V a, V b) { return V{a.x + b.x, a.y + b.y}; }
+  static __device__ __forceinline__ float get(V a, int i) { return i ? a.y : a.x; }
+};
+template <> struct RVec<64> {
+  typedef float V;
+  static __device__ __forceinline__ V load(const float* q) { return *q; }
+  static __device__ __forceinline__ V fma(V a, float w, V c) { return __builtin_fmaf(a, w, c); }
+  static __device__ __forceinline__ V add(V a, V b) { return a + b; }
+  static __device__ __forceinline__ float get(V a, int) { return a; }
+};
+
 template <typename O, int D, int NR>
 __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodeParams p) {
-  static_assert(D == 128, "two output features per lane");
+  typedef RVec<D> RV;
+  typedef typename RV::V V;
+  constexpr int FPL = D / 64;  // output features per lane
   const int row = blockIdx.x;  // (b, s, h)
   const int h = row % p.Hq;
   const int s = (row / p.Hq) % p.Sq;
   const int b = row / (p.Hq * p.Sq);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int kvh = p.map.kv_of(h);
-  const int r = s * p.G + (h - kvh * p.G);
+  const int unit = p.per_head ? h : p.map.kv_of(h);  // the work unit that computed this head
+  const int r = s * p.G + (h - unit * p.G);
   const int total_chunks = p.chunk_begin[p.nparts];
   const int total = items_of_row(p, b);  // work items (partials) of this batch row
   const int* ibegin = b < p.pair_rows ? p.item_begin : p.chunk_begin;
   const int64_t cstride = (int64_t)NR * (D + 2);
-  const float* base = p.partial + ((int64_t)b * p.Hkv + kvh) * total_chunks * cstride + r * (D + 2);
+  const float* base = p.partial + ((int64_t)b * p.units + unit) * total_chunks * cstride + r * (D + 2);
 
   __shared__ float m_s[RCH];
   __shared__ float w_s[RCH];
-  __shared__ float2 acc_s[RWAVES][D / 2];
+  __shared__ V acc_s[RWAVES][64];
 
   // the first chunk outputs of this wave, read now so their latency overlaps the statistics
   // (chunks past the end read chunk 0; unused)
-  float2 pre[RPF];
+  V pre[RPF];
 #pragma unroll
   for (int k = 0; k < RPF; ++k) {
     const int j = wave + RWAVES * k;
-    pre[k] = total > 0 ? *(const float2*)(base + (j < total ? j : 0) * cstride + 2 * lane) : float2{0.f, 0.f};
+    pre[k] = total > 0 ? RV::load(base + (j < total ? j : 0) * cstride + FPL * lane) : V{};
   }
   // items without a visible key wrote no partial: their weight is 0
   const uint64_t* cmask = p.tile_mask + (int64_t)b * total_chunks;
@@ -554,51 +579,42 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   // weighted sum of the chunk outputs over [c0, c1): wave w takes chunks w, w + 4, ...; the
   // first RPF of them came in with the statistics (pre), later ones are read when their weight
   // is known (a chunk of weight 0 is never read or used: it may hold no partial)
-  auto chunk_sum = [&](int c0, int c1) -> float2 {
-    float2 a = {0.f, 0.f};
+  auto chunk_sum = [&](int c0, int c1) -> V {
+    V a{};
 #pragma unroll
     for (int k = 0; k < RPF; ++k) {
       const int j = wave + RWAVES * k;
       if (j >= c0 && j < c1) {
         const float w = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(w_s[j])));
-        a.x = w != 0.f ? __builtin_fmaf(pre[k].x, w, a.x) : a.x;
-        a.y = w != 0.f ? __builtin_fmaf(pre[k].y, w, a.y) : a.y;
+        a = w != 0.f ? RV::fma(pre[k], w, a) : a;
       }
     }
     const int j0 = wave + RWAVES * RPF;
     for (int j = j0 + ((c0 > j0 ? c0 - j0 + RWAVES - 1 : 0) / RWAVES) * RWAVES; j < c1; j += RWAVES) {
       const float w = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(w_s[j])));
-      if (w != 0.f) {
-        const float2 o = *(const float2*)(base + j * cstride + 2 * lane);
-        a.x = __builtin_fmaf(o.x, w, a.x);
-        a.y = __builtin_fmaf(o.y, w, a.y);
-      }
+      if (w != 0.f) a = RV::fma(RV::load(base + j * cstride + FPL * lane), w, a);
     }
     acc_s[wave][lane] = a;
     __syncthreads();
-    float2 t = acc_s[0][lane];
+    V t = acc_s[0][lane];
 #pragma unroll
-    for (int i = 1; i < RWAVES; ++i) {
-      t.x += acc_s[i][lane].x;
-      t.y += acc_s[i][lane].y;
-    }
+    for (int i = 1; i < RWAVES; ++i) t = RV::add(t, acc_s[i][lane]);
     __syncthreads();
     return t;
   };
 
-  float2 res;
+  V res;
   if (p.part_out[0]) {
-    res = {0.f, 0.f};
+    res = V{};
     for (int part = 0; part < p.nparts; ++part) {
-      const float2 t = chunk_sum(ibegin[part], ibegin[part + 1]);
-      res.x += t.x;
-      res.y += t.y;
+      const V t = chunk_sum(ibegin[part], ibegin[part + 1]);
+      res = RV::add(res, t);
       if (wave == 0) {
         const bool pe = lse_p[part] == -__builtin_inff();
         const float f = pe ? 0.f : expf(lse - lse_p[part]);
         float* po = (float*)p.part_out[part] + b * p.pos_[part][0] + s * p.pos_[part][1] + h * p.pos_[part][2];
-        po[2 * lane] = t.x * f;
-        po[2 * lane + 1] = t.y * f;
+#pragma unroll
+        for (int i = 0; i < FPL; ++i) po[FPL * lane + i] = RV::get(t, i) * f;
         if (lane == 0) {
           float* pl = (float*)p.part_lse[part] + b * p.pls_[part][0] + h * p.pls_[part][1] + s * p.pls_[part][2];
           *pl = lse_p[part];
@@ -610,20 +626,21 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   }
   if (wave != 0) return;
   float* lptr = p.lse ? (float*)p.lse + b * p.ls_b + h * p.ls_h + s * p.ls_s : nullptr;
-  O* optr = (O*)p.out + b * p.os_b + s * p.os_s + h * p.os_h + 2 * lane;
+  O* optr = (O*)p.out + b * p.os_b + s * p.os_s + h * p.os_h + FPL * lane;
   if (p.accumulate) {  // merge_attention(running, new)
     const float lse_old = *lptr;
     const float lm = logaddexp<float>(lse_old, lse);
     const float safe = is_finite(lm) ? lm : 0.f;
     const float fo = expf(lse_old - safe), fn = expf(lse - safe);
-    const float v0 = add_rn(mul_rn((float)optr[0], fo), mul_rn(res.x, fn));
-    const float v1 = add_rn(mul_rn((float)optr[1], fo), mul_rn(res.y, fn));
-    optr[0] = (O)v0;
-    optr[1] = (O)v1;
+    float v[FPL];
+#pragma unroll
+    for (int i = 0; i < FPL; ++i) v[i] = add_rn(mul_rn((float)optr[i], fo), mul_rn(RV::get(res, i), fn));
+#pragma unroll
+    for (int i = 0; i < FPL; ++i) optr[i] = (O)v[i];
     if (lane == 0) *lptr = lm;  // the wave's loads of lse_old precede this store
   } else {
-    optr[0] = (O)res.x;
-    optr[1] = (O)res.y;
+#pragma unroll
+    for (int i = 0; i < FPL; ++i) optr[i] = (O)RV::get(res, i);
     if (lptr && lane == 0) *lptr = lse;
   }
 }
@@ -637,7 +654,7 @@ int launch_nr(const DecodeParams& p, hipStream_t st) {
     const hipError_t e = reserve_lds<decode_split_kernel<T, D, NR>>(DLayout<D>::LDS_BYTES);
     CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "decode: cannot reserve %d bytes of LDS: %s",
                 DLayout<D>::LDS_BYTES, hipGetErrorString(e));
-    const int64_t grid = ((int64_t)p.pair_rows * p.item_begin[p.nparts] + (int64_t)(p.B - p.pair_rows) * total) * p.Hkv;
+    const int64_t grid = ((int64_t)p.pair_rows * p.item_begin[p.nparts] + (int64_t)(p.B - p.pair_rows) * total) * p.units;
     hipLaunchKernelGGL((decode_split_kernel<T, D, NR>), dim3((unsigned)grid), dim3(DTHREADS),
                        DLayout<D>::LDS_BYTES, st, p);
     CEA_CHECK_LAUNCH("decode_split");
@@ -677,14 +694,16 @@ int decode_rows(int32_t Sq, int32_t G) {
 bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype,
                       const HeadMap& map) {
   if (!(dtype == CEA_BF16 || dtype == CEA_F16)) return false;
-  if (D != 128) return false;
-  if (map.group <= 0) return false;  // regular GQA grouping only
-  return decode_rows(Sq, Hq / Hkv) != 0;
+  if (!(D == 64 || D == 128)) return false;
+  // the regular grouping shares each K/V row among the G query heads of a KV head; any other
+  // map runs one unit per query head
+  if (map.group > 0) return decode_rows(Sq, Hq / Hkv) != 0;
+  return Hq <= CEA_MAX_MAPPED_HEADS && decode_rows(Sq, 1) != 0;
 }
 
-int decode_plan_chunk(int64_t keys_per_head, int32_t B, int32_t Hkv) {
+int decode_plan_chunk(int64_t keys_per_head, int32_t B, int32_t units) {
   // enough work items to fill 256 CUs several times, chunks of 256..1024 keys
-  const int64_t heads = (int64_t)B * Hkv;
+  const int64_t heads = (int64_t)B * units;
   int ch = 256;
   while (ch < CHMAX && heads * ((keys_per_head + ch - 1) / ch) > CEA_DECODE_ITEMS) ch *= 2;
   return ch;
@@ -703,13 +722,15 @@ int launch_attn_decode(const DecodeParams& params, hipStream_t st) {
   p.item_begin[0] = 0;
   for (int i = 0; i < p.nparts; ++i)
     p.item_begin[i + 1] = p.item_begin[i] + (p.chunk_begin[i + 1] - p.chunk_begin[i] + 1) / 2;
-  const int64_t row_items = (int64_t)p.Hkv * p.chunk_begin[p.nparts];
+  const int64_t row_items = (int64_t)p.units * p.chunk_begin[p.nparts];
   const bool pairs = p.chunk == CHMAX && p.B * row_items >= CEA_DECODE_ITEMS;
   const int cus = device_cus();
   const int64_t tail_rows = row_items > 0 ? (4 * (int64_t)(cus > 0 ? cus : 256) + row_items - 1) / row_items : 1;
   p.pair_rows = pairs ? (int)max((int64_t)0, (int64_t)p.B - tail_rows) : 0;
   if (p.D == 128 && p.in_dtype == CEA_BF16) return launch_d<bf16, 128>(p, nr, st);
   if (p.D == 128 && p.in_dtype == CEA_F16) return launch_d<f16, 128>(p, nr, st);
+  if (p.D == 64 && p.in_dtype == CEA_BF16) return launch_d<bf16, 64>(p, nr, st);
+  if (p.D == 64 && p.in_dtype == CEA_F16) return launch_d<f16, 64>(p, nr, st);
   set_error("decode: unsupported dtype %s / head size %d", dtype_name(p.in_dtype), p.D);
   return CEA_EUNSUPPORTED;
 }

@@ -153,20 +153,50 @@ struct DecodePlan {
   size_t vis_offset, mask_offset;
 };
 
-static DecodePlan plan_decode(const int64_t* Sk, int n, int64_t B, int64_t Sq, int64_t Hq,
-                              int64_t Hkv, int64_t D) {
+// Work units of the decode kernels for a head map: the KV heads (G = Hq / Hkv query heads
+// each) for the regular grouping, the query heads (G = 1) for any other map.
+struct DecodeUnits {
+  int32_t units, G, per_head;
+};
+static DecodeUnits decode_units(int64_t Hq, int64_t Hkv, const HeadMap& map) {
+  if (map.group > 0) return {(int32_t)Hkv, (int32_t)(Hq / Hkv), 0};
+  return {(int32_t)Hq, 1, 1};
+}
+
+static DecodePlan plan_decode(const int64_t* Sk, int n, int64_t B, int64_t Sq, int64_t units,
+                              int64_t G, int64_t D) {
   DecodePlan pl;
   int64_t keys = 0;
   for (int i = 0; i < n; ++i) keys += Sk[i];
-  pl.chunk = decode_plan_chunk(keys, (int32_t)B, (int32_t)Hkv);
+  pl.chunk = decode_plan_chunk(keys, (int32_t)B, (int32_t)units);
   pl.total_chunks = 0;
   for (int i = 0; i < n; ++i) pl.total_chunks += (int)((Sk[i] + pl.chunk - 1) / pl.chunk);
-  pl.nr = decode_rows((int32_t)Sq, (int32_t)(Hq / (Hkv > 0 ? Hkv : 1)));
-  pl.vis_offset = align_up((size_t)(B * Hkv) * pl.total_chunks * (pl.nr > 0 ? pl.nr : 1) *
+  pl.nr = decode_rows((int32_t)Sq, (int32_t)G);
+  pl.vis_offset = align_up((size_t)(B * units) * pl.total_chunks * (pl.nr > 0 ? pl.nr : 1) *
                                (D + 2) * sizeof(float), 256);
   pl.mask_offset = pl.vis_offset + align_up((size_t)B * pl.total_chunks * pl.chunk * sizeof(uint16_t), 256);
   pl.partial_bytes = pl.mask_offset + align_up((size_t)B * pl.total_chunks * sizeof(uint64_t), 256);
   return pl;
+}
+
+// Decode scratch of the largest plan a call of these shapes can take, for callers that do not
+// pass the head map: the regular grouping's plan and the per-query-head plan of any other map,
+// and none for dtypes or head sizes the decode kernels do not take.
+static size_t decode_ws_bytes(const int64_t* Sk, int n, int64_t B, int64_t Sq, int64_t Hq,
+                              int64_t Hkv, int64_t D, int32_t dtype) {
+  HeadMap regular;
+  regular.group = 1;
+  size_t need = 0;
+  if (Hkv > 0 && Hq % Hkv == 0 &&
+      decode_supported((int32_t)Sq, (int32_t)Hq, (int32_t)Hkv, (int32_t)D, dtype, regular))
+    need = plan_decode(Sk, n, B, Sq, Hkv, Hq / Hkv, D).partial_bytes;
+  HeadMap table;
+  table.group = 0;
+  if (Hkv > 0 && decode_supported((int32_t)Sq, (int32_t)Hq, (int32_t)Hkv, (int32_t)D, dtype, table)) {
+    const size_t ph = plan_decode(Sk, n, B, Sq, Hq, 1, D).partial_bytes;
+    need = ph > need ? ph : need;
+  }
+  return need;
 }
 
 // Fills a DecodeParams from n per-block parameter blocks (same q, q_pos, out, lse).
@@ -175,7 +205,8 @@ static int run_decode(const AttnParams* blocks, int n, cea_tensor* part_out, cea
   const AttnParams& a = blocks[0];
   int64_t sks[CEA_MAX_PARTS];
   for (int i = 0; i < n; ++i) sks[i] = blocks[i].Sk;
-  const DecodePlan pl = plan_decode(sks, n, a.B, a.Sq, a.Hq, a.Hkv, a.D);
+  const DecodeUnits du = decode_units(a.Hq, a.Hkv, a.map);
+  const DecodePlan pl = plan_decode(sks, n, a.B, a.Sq, du.units, du.G, a.D);
   CEA_REQUIRE(ws != nullptr && ws_bytes >= pl.partial_bytes, CEA_ENOSPACE,
               "decode: workspace of %zu bytes needed, %zu given", pl.partial_bytes, ws_bytes);
   DecodeParams d;
@@ -211,7 +242,9 @@ static int run_decode(const AttnParams* blocks, int n, cea_tensor* part_out, cea
   d.partial = (float*)ws;
   d.vis = (uint16_t*)(ws + pl.vis_offset);
   d.tile_mask = (uint64_t*)(ws + pl.mask_offset);
-  d.G = a.Hq / a.Hkv;
+  d.G = du.G;
+  d.units = du.units;
+  d.per_head = du.per_head;
   d.out = a.out; d.lse = a.lse;
   d.os_b = a.os_b; d.os_s = a.os_s; d.os_h = a.os_h;
   d.ls_b = a.ls_b; d.ls_h = a.ls_h; d.ls_s = a.ls_s;
@@ -223,7 +256,8 @@ static int run_decode(const AttnParams* blocks, int n, cea_tensor* part_out, cea
 static bool use_decode(const AttnParams& p) {
   if (!decode_supported(p.Sq, p.Hq, p.Hkv, p.D, p.in_dtype, p.map)) return false;
   const int64_t sk = p.Sk;
-  if (plan_decode(&sk, 1, p.B, p.Sq, p.Hq, p.Hkv, p.D).total_chunks > kDecodeMaxChunks) return false;
+  const DecodeUnits du = decode_units(p.Hq, p.Hkv, p.map);
+  if (plan_decode(&sk, 1, p.B, p.Sq, du.units, du.G, p.D).total_chunks > kDecodeMaxChunks) return false;
   if (!(p.out_dtype == CEA_F32 || p.out_dtype == p.in_dtype)) return false;
   if (p.accumulate && p.out_dtype != CEA_F32) return false;
   if (!(fabs(p.scale) >= 1e-30 && fabs(p.scale) <= 1e30)) return false;
@@ -305,14 +339,10 @@ int cea_version(void) { return 100; }
 
 size_t cea_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int64_t Hkv,
                                      int64_t D, int32_t in_dtype) {
-  (void)in_dtype;
   if (B <= 0 || Sk <= 0) return 256;
   size_t need = tile_bytes(B, Sk);
-  if (Hkv > 0 && Hq % Hkv == 0 && decode_rows((int32_t)Sq, (int32_t)(Hq / Hkv)) > 0) {
-    const size_t dec = plan_decode(&Sk, 1, B, Sq, Hq, Hkv, D).partial_bytes;
-    need = dec > need ? dec : need;
-  }
-  return need;
+  const size_t dec = decode_ws_bytes(&Sk, 1, B, Sq, Hq, Hkv, D, in_dtype);
+  return dec > need ? dec : need;
 }
 
 int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
@@ -803,7 +833,6 @@ int cea_ulysses_gather(int32_t n, const cea_tensor* outs, int64_t token_start, c
 size_t cea_partitioned_attention_workspace_bytes(int32_t n, const int64_t* Sk, int64_t B,
                                                  int64_t Sq, int64_t Hq, int64_t Hkv, int64_t D,
                                                  int32_t in_dtype) {
-  (void)Hkv;
   if (n <= 0 || n > CEA_MAX_PARTS || B <= 0) return 256;
   const size_t esz = in_dtype == CEA_F64 ? 8 : 4;
   size_t need = 0;
@@ -813,11 +842,8 @@ size_t cea_partitioned_attention_workspace_bytes(int32_t n, const int64_t* Sk, i
   // per-partition partials (out, lse) in the accumulation dtype
   need += (size_t)n * align_up((size_t)(B * Sq * Hq * D) * esz, 256);
   need += (size_t)n * align_up((size_t)(B * Hq * Sq) * esz, 256);
-  if (Hkv > 0 && Hq % Hkv == 0 && decode_rows((int32_t)Sq, (int32_t)(Hq / Hkv)) > 0) {
-    const size_t dec = plan_decode(Sk, n, B, Sq, Hq, Hkv, D).partial_bytes;
-    need = dec > need ? dec : need;
-  }
-  return need;
+  const size_t dec = decode_ws_bytes(Sk, n, B, Sq, Hq, Hkv, D, in_dtype);
+  return dec > need ? dec : need;
 }
 
 int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* ks,
@@ -859,7 +885,10 @@ int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* 
       if (rc) return rc;
       dec = dec && use_decode(blocks[i]);
     }
-    dec = dec && plan_decode(sks, n, B, Sq, Hq, blocks[0].Hkv, D).total_chunks <= kDecodeMaxChunks;
+    if (dec) {
+      const DecodeUnits du = decode_units(Hq, blocks[0].Hkv, blocks[0].map);
+      dec = plan_decode(sks, n, B, Sq, du.units, du.G, D).total_chunks <= kDecodeMaxChunks;
+    }
     if (dec && part_out) {
       for (int i = 0; i < n && rc == 0; ++i) {
         rc = check_tensor(&part_out[i], "part_out", 4, acc, true);

@@ -104,6 +104,11 @@ struct DecodeParams {
   uint16_t* vis;
   uint64_t* tile_mask;
   int32_t G;                 // query heads per KV head handled by one work item
+  // work units per batch row: the KV heads (G query heads each, kv = h / G), or, for an
+  // explicit head map that is not that grouping (per_head = 1), the query heads themselves
+  // (G = 1; unit h reads KV head map.kv[h])
+  int32_t units;
+  int32_t per_head;
   // outputs of the reduction
   void* part_out[CEA_MAX_PARTS];   // optional per-partition (out, lse), f32
   void* part_lse[CEA_MAX_PARTS];
@@ -200,7 +205,7 @@ int launch_attn_f32_mfma(const AttnParams& p, hipStream_t s);
 bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype,
                       const HeadMap& map);
 constexpr int kDecodeMaxChunks = 1024;  // key chunks per (batch, kv head), all partitions
-int decode_plan_chunk(int64_t total_keys, int32_t B, int32_t Hkv);
+int decode_plan_chunk(int64_t total_keys, int32_t B, int32_t units);
 int decode_rows(int32_t Sq, int32_t G);  // padded query rows per kv head, 0 = unsupported
 int launch_attn_decode(const DecodeParams& p, hipStream_t s);
 

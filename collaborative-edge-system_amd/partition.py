@@ -19,6 +19,8 @@ messages; on one GPU they decide which blocks a simulated rank streams.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import bisect
 import heapq
 import itertools
@@ -92,11 +94,13 @@ def offsets_of(sizes: Sequence[int]) -> List[int]:
 # --------------------------------------------------------------------------------------
 # attention heads
 # --------------------------------------------------------------------------------------
-class HeadShard(NamedTuple):
+@dataclass(frozen=True)
+class HeadShard:
     """Query heads ``[q_start, q_start + q_count)`` of one rank and the KV heads
     ``[kv_start, kv_start + kv_count)`` they read (partition.py:83-105).  ``kv_map[i]`` is the
     shard-local KV head of the ``i``-th local query head; a KV head needed by several ranks
-    appears in each of their shards."""
+    appears in each of their shards.  A frozen dataclass with the reference's fields, so
+    ``dataclasses.fields`` / ``replace`` / ``asdict`` and equality behave as there."""
 
     q_start: int
     q_count: int
@@ -251,10 +255,21 @@ class SequenceLayout:
         for r, p in enumerate(parts):
             if p.shape[dim] != self.sizes[r]:
                 raise ValueError(f"part {r} holds {p.shape[dim]} tokens, the layout gives it {self.sizes[r]}")
+        # what the reference's torch.cat of the pieces does: the other dimensions and the
+        # device must agree (RuntimeError otherwise), mixed dtypes promote
         ref = parts[0]
+        d = dim % ref.dim() if ref.dim() else dim
+        dtype = ref.dtype
+        for r, p in enumerate(parts[1:], 1):
+            if p.dim() != ref.dim() or any(a != b for i, (a, b) in enumerate(zip(p.shape, ref.shape)) if i != d):
+                raise RuntimeError(f"part {r} has shape {tuple(p.shape)}, part 0 {tuple(ref.shape)}: "
+                                   f"sizes must match except in dimension {d}")
+            if p.device != ref.device:
+                raise RuntimeError(f"part {r} is on {p.device}, part 0 on {ref.device}")
+            dtype = torch.promote_types(dtype, p.dtype)
         shape = list(ref.shape)
         shape[dim] = self.seq_len
-        full = ref.new_empty(shape)
+        full = ref.new_empty(shape, dtype=dtype)
         for c in self._chunks:
             full.narrow(dim, c.start, c.length).copy_(parts[c.rank].narrow(dim, c.local, c.length))
         return full

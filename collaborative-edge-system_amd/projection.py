@@ -22,7 +22,8 @@ kernel.
 
 from __future__ import annotations
 
-from typing import List, Optional, Sequence, Tuple
+import itertools
+from typing import List, NamedTuple, Optional, Sequence, Tuple
 
 import torch
 import torch.nn as nn
@@ -82,27 +83,54 @@ def linear_gated(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
     return nat.ops().linear_gated(x, w_gate, w_up, b_gate, b_up, ACTIVATION_CODES[act])
 
 
+class _Slice(NamedTuple):
+    """One projection of a fused layer: its full width ``full``, the rows ``[start, start +
+    size)`` of it this rank holds, and the first row ``row0`` of those in the fused weight."""
+
+    full: int
+    start: int
+    size: int
+    row0: int
+
+
+def _slices(parts: Sequence[Tuple[int, int, int]]) -> List[_Slice]:
+    """The fused weight's row layout: local slices stacked in part order.  Raises ValueError
+    naming every part whose local range leaves ``[0, out_features)``."""
+    triples = [tuple(int(v) for v in t) for t in parts]
+    bad = [f"part {i}: ({s}, {n}) outside [0, {o})" for i, (o, s, n) in enumerate(triples)
+           if s < 0 or n < 0 or s + n > o]
+    if bad:
+        raise ValueError("local range outside the projection: " + "; ".join(bad))
+    starts = itertools.accumulate((n for _, _, n in triples), initial=0)
+    return [_Slice(o, s, n, r) for (o, s, n), r in zip(triples, starts)]
+
+
 class FusedColumnParallelLinear(nn.Module):
     """Several column-parallel projections of one input computed by one GEMM
     (tensor_parallel.py:264-313).  ``parts`` lists ``(out_features, local_start, local_size)``
-    per projection; :meth:`forward` returns the per-projection outputs."""
+    per projection; :meth:`forward` returns the per-projection outputs as column views of
+    the one GEMM result."""
 
     def __init__(self, in_features: int, parts: Sequence[Tuple[int, int, int]], comm=None, *,
                  bias: bool = False, dtype: Optional[torch.dtype] = None,
                  device: Optional[torch.device] = None) -> None:
         super().__init__()
         self.comm = comm
-        self.in_features = in_features
-        self.parts = [(int(o), int(s), int(n)) for o, s, n in parts]
-        for out, start, size in self.parts:
-            if start < 0 or size < 0 or start + size > out:
-                raise ValueError(f"local range ({start}, {size}) outside [0, {out})")
-        self.local_sizes = [n for _, _, n in self.parts]
-        total = sum(self.local_sizes)
-        self.weight = nn.Parameter(torch.empty(total, in_features, dtype=dtype, device=device),
-                                   requires_grad=False)
-        self.bias = (nn.Parameter(torch.empty(total, dtype=dtype, device=device), requires_grad=False)
-                     if bias else None)
+        self.in_features = int(in_features)
+        self._slices = _slices(parts)
+        rows = sum(sl.size for sl in self._slices)
+        make = lambda *shape: nn.Parameter(torch.empty(*shape, dtype=dtype, device=device),
+                                           requires_grad=False)
+        self.weight = make(rows, self.in_features)
+        self.bias = make(rows) if bias else None
+
+    @property
+    def parts(self) -> List[Tuple[int, int, int]]:
+        return [(sl.full, sl.start, sl.size) for sl in self._slices]
+
+    @property
+    def local_sizes(self) -> List[int]:
+        return [sl.size for sl in self._slices]
 
     def forward(self, x: torch.Tensor) -> List[torch.Tensor]:
         return fused_linear(x, self.weight, self.bias, self.local_sizes)
@@ -112,39 +140,45 @@ class FusedColumnParallelLinear(nn.Module):
         ``gate, up = self(x); h = act(gate) * up`` (llama.py:302-305).  ``units = (start,
         count)`` restricts it to a slice of the local units, as the replicated-token branch
         does (llama.py:309-316)."""
-        if len(self.local_sizes) != 2 or self.local_sizes[0] != self.local_sizes[1]:
+        if len(self._slices) != 2 or self._slices[0].size != self._slices[1].size:
             raise ValueError("gated() needs two equal parts: gate and up")
-        n = self.local_sizes[0]
-        start, count = units if units is not None else (0, n)
-        if start < 0 or count < 0 or start + count > n:
-            raise ValueError(f"units ({start}, {count}) outside [0, {n})")
+        gate, up = self._slices
+        start, count = units if units is not None else (0, gate.size)
+        if start < 0 or count < 0 or start + count > gate.size:
+            raise ValueError(f"units ({start}, {count}) outside [0, {gate.size})")
+        rows_g = slice(gate.row0 + start, gate.row0 + start + count)
+        rows_u = slice(up.row0 + start, up.row0 + start + count)
         w, b = self.weight, self.bias
-        return linear_gated(x, w[start:start + count], w[n + start:n + start + count],
-                            None if b is None else b[start:start + count],
-                            None if b is None else b[n + start:n + start + count], act)
+        return linear_gated(x, w[rows_g], w[rows_u], None if b is None else b[rows_g],
+                            None if b is None else b[rows_u], act)
 
     @torch.no_grad()
     def load_full(self, weights: Sequence[torch.Tensor],
                   biases: Optional[Sequence[Optional[torch.Tensor]]] = None) -> None:
-        """Load from the full (unsharded) parameters of every fused projection."""
-        if len(weights) != len(self.parts):
-            raise ValueError(f"expected {len(self.parts)} weights, got {len(weights)}")
-        offset = 0
-        for i, (_, start, size) in enumerate(self.parts):
-            src = weights[i].narrow(0, start, size)
-            dst = self.weight[offset:offset + size]
-            if tuple(dst.shape) != tuple(src.shape):
-                raise ValueError(f"shape mismatch: parameter {tuple(dst.shape)} vs value {tuple(src.shape)}")
-            dst.copy_(src.to(dtype=dst.dtype, device=dst.device))
-            if self.bias is not None:
-                if biases is None or biases[i] is None:
-                    raise ValueError("layer has a bias but none was provided")
-                self.bias[offset:offset + size].copy_(
-                    biases[i].narrow(0, start, size).to(dtype=self.bias.dtype, device=self.bias.device))
-            offset += size
+        """Fill the fused parameters from the full (unsharded) parameters of every projection:
+        this rank's rows of each, stacked in part order, copied in one go."""
+        if len(weights) != len(self._slices):
+            raise ValueError(f"expected {len(self._slices)} weights, got {len(weights)}")
+        if self.bias is not None and (biases is None or len(biases) != len(self._slices)
+                                      or any(t is None for t in biases)):
+            raise ValueError("layer has a bias but none was provided")
+
+        def stacked(full: Sequence[torch.Tensor], param: torch.Tensor) -> torch.Tensor:
+            rows = [t.narrow(0, sl.start, sl.size).to(param.device, param.dtype)
+                    for t, sl in zip(full, self._slices)]
+            got = torch.cat(rows, 0)
+            if got.shape != param.shape:
+                raise ValueError(f"shape mismatch: parameter {tuple(param.shape)} vs value {tuple(got.shape)}")
+            return got
+
+        self.weight.copy_(stacked(weights, self.weight))
+        if self.bias is not None:
+            self.bias.copy_(stacked(biases, self.bias))
 
     def extra_repr(self) -> str:
-        return f"in={self.in_features}, parts={self.parts}, bias={self.bias is not None}"
+        layout = ", ".join(f"{sl.size} of {sl.full} from {sl.start}" for sl in self._slices)
+        return (f"in_features={self.in_features}, rows={self.weight.shape[0]} ({layout}), "
+                f"bias={self.bias is not None}")
 
 
 __all__ = ["FusedColumnParallelLinear", "fused_linear", "linear", "linear_gated"]

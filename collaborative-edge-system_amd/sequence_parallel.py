@@ -259,8 +259,6 @@ def partitioned_attention(
     parts = list(parts)
     if not parts:
         raise ValueError("need at least one partition")
-    if len(parts) > nat.MAX_PARTS:
-        raise NotImplementedError(f"at most {nat.MAX_PARTS} partitions per call")
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
     mapping = _kv_map_list(kv_map)
     for p in parts:
@@ -268,6 +266,21 @@ def partitioned_attention(
     acc = accumulation_dtype(q.dtype)
     if out_dtype is None:  # the merged lse comes with an accumulation-precision output
         out_dtype = acc if return_lse else q.dtype
+    if len(parts) > nat.MAX_PARTS:
+        # more partitions than one launch takes: groups of up to MAX_PARTS, each one split-KV
+        # launch with its reduction, then the exact merge of the groups (the merge is
+        # associative; the reference merges all partials at once, attention.py:253-264)
+        groups = [partitioned_attention(q, q_pos, parts[i:i + nat.MAX_PARTS], causal=causal,
+                                        scale=scale, kv_map=mapping, out_dtype=acc,
+                                        return_lse=True, return_parts=return_parts)
+                  for i in range(0, len(parts), nat.MAX_PARTS)]
+        out, lse = merge_attention_list([g[0] for g in groups], [g[1] for g in groups])
+        result = [out.to(out_dtype)]
+        if return_lse:
+            result.append(lse)
+        if return_parts:
+            result.append([pr for g in groups for pr in g[2]])
+        return result[0] if len(result) == 1 else tuple(result)
     res = nat.ops().partitioned(q, q_pos, [p[0] for p in parts], [p[1] for p in parts],
                                 [p[2] for p in parts], bool(causal), scale, mapping, out_dtype,
                                 bool(return_lse), bool(return_parts))

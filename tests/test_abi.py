@@ -214,3 +214,21 @@ def test_missing_libraries_fail_loudly(cea, monkeypatch, tmp_path):
     monkeypatch.setattr(nat, "OPS_PATH", tmp_path / "libcollab_edge_torch.so")
     with pytest.raises(RuntimeError, match="missing: build it"):
         nat.ops()
+
+
+def test_workspace_counts_decode_partials_only_for_the_decode_route(cea):
+    """cea_attention_workspace_bytes adds the split-KV decode partials only for calls the
+    decode kernels take (bf16 / f16, head size 64 or 128): f32 and f64 calls of a decode shape
+    need the tile summaries alone, so the no-allocation entry point does not refuse them."""
+    nat = cea._native
+    lib = nat.load_library()
+    B, Hq, Sk, Hkv, D = 64, 32, 32768, 8, 128
+    tiles = B * ((Sk + 63) // 64) * 32
+    bf16 = lib.cea_attention_workspace_bytes(B, 1, Hq, Sk, Hkv, D, 1)
+    f32 = lib.cea_attention_workspace_bytes(B, 1, Hq, Sk, Hkv, D, 0)
+    f64 = lib.cea_attention_workspace_bytes(B, 1, Hq, Sk, Hkv, D, 3)
+    odd = lib.cea_attention_workspace_bytes(B, 1, Hq, Sk, Hkv, 96, 1)
+    assert bf16 > (32 << 20) > f32
+    assert f32 == f64 == odd == tiles
+    # head size 64 takes the decode route as well
+    assert lib.cea_attention_workspace_bytes(B, 1, Hq, Sk, Hkv, 64, 1) > tiles

@@ -124,3 +124,37 @@ def test_kv_append_argument_errors(cea, dev):
         cea.kv_append(ck, ck.clone(), cp, 0, k, k, pos, torch.ones(1, 4, 8, device=dev), None)
     with pytest.raises(RuntimeError):  # host tensors are refused, never computed on the CPU
         cea.kv_append(ck.cpu(), ck.cpu(), cp.cpu(), 0, k.cpu(), k.cpu(), pos.cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_values_with_their_own_heads_and_size(cea, dev, dtype):
+    """V with another head count and head size than K (cache.py:42-43 sizes V from V): the
+    cache keeps V in an allocation of its own; K is rotated by the rotary kernel; the cached
+    tensors equal the oracle's bit for bit through a growth sequence of rotary and plain
+    appends."""
+    B, Hk, Dk, Hv, Dv = 2, 4, 64, 2, 96
+    inv = L.inv_freq(Dk, 1e4, dtype=torch.float32)
+    gc, rc = cea.LayerKVCache(reserve=2), C.LayerKVCache(reserve=2)
+    t = 0
+    for i, n in enumerate([4, 9, 1, 20]):
+        g = _gen(40 + i)
+        k = torch.randn(B, n, Hk, Dk, generator=g).to(dtype)
+        v = torch.randn(B, n, Hv, Dv, generator=g).to(dtype)
+        pos = torch.arange(t, t + n).repeat(B, 1)
+        if i % 2 == 0:
+            cos, sin = L.rope_tables(pos, inv, dtype)
+            gc.append_rotary(k.to(dev), v.to(dev), pos.to(dev), cos.to(dev), sin.to(dev))
+            rc.append_rotary(k, v, pos, cos, sin)
+        else:
+            gc.append(k.to(dev), v.to(dev), pos.to(dev))
+            rc.append(k, v, pos)
+        t += n
+    torch.cuda.synchronize()
+    assert tuple(gc.v.shape[1::2]) == (Hv, Dv) and tuple(gc.k.shape[1::2]) == (Hk, Dk)
+    _same(gc, rc)
+    assert gc.nbytes() == B * t * (Hk * Dk + Hv * Dv) * torch.empty(0, dtype=dtype).element_size()
+    assert gc.capacity >= t + 2  # the next append fits: the shape check, not a regrowth, refuses it
+    with pytest.raises(ValueError):  # a later V of yet another shape
+        gc.append(torch.zeros(B, 2, Hk, Dk, dtype=dtype, device=dev),
+                  torch.zeros(B, 2, Hv, Dk, dtype=dtype, device=dev),
+                  torch.arange(t, t + 2).repeat(B, 1).to(dev))

@@ -122,23 +122,36 @@ def test_ring_share_with_wire_compression(cea, dev, wire):
 
 
 DECODE_CASES = [
-    # (B, Sq, Hq, Hkv, cap, parts)
-    (3, 1, 32, 8, 700, [400, 300]),
-    (2, 1, 8, 8, 1500, [1500]),
-    (2, 2, 8, 4, 999, [333, 333, 333]),
-    (2, 4, 4, 4, 513, [100, 13, 400]),
-    (1, 1, 16, 4, 5000, [2000, 1500, 1000, 500]),
+    # (B, Sq, Hq, Hkv, cap, parts, D, kv_map)
+    (3, 1, 32, 8, 700, [400, 300], 128, None),
+    (2, 1, 8, 8, 1500, [1500], 128, None),
+    (2, 2, 8, 4, 999, [333, 333, 333], 128, None),
+    (2, 4, 4, 4, 513, [100, 13, 400], 128, None),
+    (1, 1, 16, 4, 5000, [2000, 1500, 1000, 500], 128, None),
+    # head size 64: the tinyllama-1.1b (32/4) and qwen2-0.5b (14/2) presets
+    # (models/config.py:18,21), multi-query with four new tokens
+    (3, 1, 32, 4, 700, [400, 300], 64, None),
+    (2, 1, 14, 2, 999, [333, 333, 333], 64, None),
+    (1, 4, 4, 1, 513, [100, 413], 64, None),
+    # explicit maps that are not the h // g grouping: shard 0 of partition_heads(32, 8, 3)
+    # (groups of 4, 4, 3; partition.py:141-152) and an arbitrary one
+    (2, 2, 11, 3, 800, [500, 300], 128, [0, 0, 0, 0, 1, 1, 1, 1, 2, 2, 2]),
+    (2, 1, 6, 2, 600, [600], 64, [1, 0, 0, 1, 1, 0]),
 ]
 
 
+def _case_id(s):
+    return "B{}-Sq{}-H{}/{}-cap{}-p{}-D{}{}".format(*s[:5], len(s[5]), s[6], "-map" if s[7] else "")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
-@pytest.mark.parametrize("shape", DECODE_CASES, ids=lambda s: "B{}-Sq{}-H{}/{}-cap{}-p{}".format(*s[:5], len(s[5])))
+@pytest.mark.parametrize("shape", DECODE_CASES, ids=_case_id)
 def test_partitioned_decode_matches_oracle(cea, dev, shape, dtype):
-    Bn, Sq, Hq, Hkv, cap, sizes = shape
-    g = torch.Generator().manual_seed(sum(sizes) + Sq)
-    ck = torch.randn(Bn, Hkv, cap, 128, generator=g).to(dtype)
-    cv = torch.randn(Bn, Hkv, cap, 128, generator=g).to(dtype)
-    q = torch.randn(Bn, Sq, Hq, 128, generator=g).to(dtype)
+    Bn, Sq, Hq, Hkv, cap, sizes, d, kv_map = shape
+    g = torch.Generator().manual_seed(sum(sizes) + Sq + d)
+    ck = torch.randn(Bn, Hkv, cap, d, generator=g).to(dtype)
+    cv = torch.randn(Bn, Hkv, cap, d, generator=g).to(dtype)
+    q = torch.randn(Bn, Sq, Hq, d, generator=g).to(dtype)
     lens = torch.randint(1, cap + 1, (Bn,), generator=g)
     slots = torch.arange(cap).view(1, cap)
     kpos = torch.where(slots < lens.view(-1, 1), slots, torch.full_like(slots, -1))
@@ -152,19 +165,19 @@ def test_partitioned_decode_matches_oracle(cea, dev, shape, dtype):
         parts_cpu.append((ck[:, :, start:start + n].transpose(1, 2), cv[:, :, start:start + n].transpose(1, 2),
                           kpos[:, start:start + n]))
         start += n
-    out, lse, per = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts, return_lse=True,
-                                              return_parts=True)
-    out_q = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts)
-    ro, rl, rparts = sp_ref.distributed_kv_share(q, qpos, parts_cpu, with_parts=True)
+    out, lse, per = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts, kv_map=kv_map,
+                                              return_lse=True, return_parts=True)
+    out_q = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts, kv_map=kv_map)
+    ro, rl, rparts = sp_ref.distributed_kv_share(q, qpos, parts_cpu, kv_map=kv_map, with_parts=True)
     torch.cuda.synchronize()
     assert out_q.dtype == dtype
     for (po, pl), (qo, ql) in zip(per, rparts):
         assert_attention_close(po, pl, qo, ql, dtype, "partition")
     assert_attention_close(out, lse, ro.float(), rl, dtype, "merged")
     assert (out_q.cpu().float() - ro.float()).abs().max().item() <= 2e-2
-    # single-partition attention_with_lse on the decode path (and its kv_block variant)
-    o1, l1 = cea.attention_with_lse(q.to(dev), *parts[0][:2], qpos.to(dev), parts[0][2])
-    r1, s1 = ref.attention_with_lse(q, *parts_cpu[0][:2], qpos, parts_cpu[0][2])
+    # single-partition attention_with_lse on the decode path
+    o1, l1 = cea.attention_with_lse(q.to(dev), *parts[0][:2], qpos.to(dev), parts[0][2], kv_map=kv_map)
+    r1, s1 = ref.attention_with_lse(q, *parts_cpu[0][:2], qpos, parts_cpu[0][2], kv_map=kv_map)
     torch.cuda.synchronize()
     assert_attention_close(o1, l1, r1, s1, dtype, "single partition")
 
@@ -281,3 +294,40 @@ def test_partitioned_decode_chunk_pairs_two_tokens(cea, dev):
         for i, ((po, pl), (qo, ql)) in enumerate(zip(per, rparts)):
             assert_attention_close(po[sl], pl[sl], qo, ql, torch.bfloat16, f"seq {b} partition {i}")
         assert_attention_close(out[sl], lse[sl], ro.float(), rl, torch.bfloat16, f"seq {b} merged")
+
+
+@pytest.mark.parametrize("nranks", [17, 40])
+def test_distributed_kv_more_ranks_than_one_launch(cea, dev, nranks):
+    """A cache sharded over more ranks than one split-KV launch takes (16): the partitions run
+    in groups, each group merged in its reduction, and the groups merged exactly; the result,
+    the merged lse and every rank's partial (out, lse) match the oracle's all-at-once merge
+    (sequence_parallel.py:273-279 -> attention.py:253-264)."""
+    B, hq, hkv, d, cap = 2, 8, 2, 128, 3000
+    g = torch.Generator().manual_seed(nranks)
+    k = torch.randn(B, cap, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, cap, hkv, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, 1, hq, d, generator=g).to(torch.bfloat16)
+    lens = torch.tensor([cap, 1700])
+    slots = torch.arange(cap).view(1, cap)
+    pos = torch.where(slots < lens.view(-1, 1), slots, torch.full_like(slots, -1))
+    qpos = (lens - 1).view(-1, 1)
+    sizes = cea.split_sizes(cap, nranks)
+    group = cea.LocalGroup(nranks, 3)
+    parts_cpu, start = [], 0
+    for r, n in enumerate(sizes):
+        parts_cpu.append((k[:, start:start + n], v[:, start:start + n], pos[:, start:start + n]))
+        group.set_shard(r, k=parts_cpu[-1][0].to(dev), v=parts_cpu[-1][1].to(dev),
+                        pos=parts_cpu[-1][2].to(dev))
+        start += n
+    own = group.shard(3)
+    out = cea.distributed_kv_attention(q.to(dev), own["k"], own["v"], qpos.to(dev), own["pos"], group)
+    parts = [tuple(group.shard(r)[x] for x in ("k", "v", "pos")) for r in range(nranks)]
+    o2, l2, per = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts, return_lse=True,
+                                            return_parts=True)
+    ro, rl, rparts = sp_ref.distributed_kv_share(q, qpos, parts_cpu, with_parts=True)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and len(per) == nranks
+    assert (out.cpu().float() - ro.float()).abs().max().item() <= 2e-2
+    assert_attention_close(o2, l2, ro.float(), rl, torch.bfloat16, f"{nranks} ranks merged")
+    for i, ((po, pl), (qo, ql)) in enumerate(zip(per, rparts)):
+        assert_attention_close(po, pl, qo, ql, torch.bfloat16, f"rank {i} partial")

@@ -368,3 +368,59 @@ def test_gather_sequence_restores_global_order(cea, kind):
         assert torch.equal(got, x)
     single = cea.LocalGroup(1)
     assert cea.gather_sequence(x, cea.SequenceLayout(S, 1), single) is x
+
+
+def test_head_shard_is_the_reference_dataclass():
+    """HeadShard keeps the reference's frozen dataclass (partition.py:83-105): field names and
+    order, immutability, dataclasses.replace / asdict, equality by value (not with a tuple)."""
+    import dataclasses
+
+    sh = cea.partition_heads(32, 8, 3)
+    assert dataclasses.is_dataclass(sh[0])
+    assert [f.name for f in dataclasses.fields(sh[0])] == ["q_start", "q_count", "kv_start",
+                                                            "kv_count", "kv_map"]
+    with pytest.raises(dataclasses.FrozenInstanceError):
+        sh[0].q_count = 3
+    assert dataclasses.replace(sh[0], q_count=2).q_count == 2
+    assert dataclasses.asdict(sh[2])["kv_map"] == sh[2].kv_map
+    assert sh[0] != tuple(dataclasses.astuple(sh[0]))
+    assert sh[1].q_range == (sh[1].q_start, sh[1].q_start + sh[1].q_count)
+    assert sh[1].kv_range == (sh[1].kv_start, sh[1].kv_start + sh[1].kv_count)
+
+
+def test_unshard_behaves_like_cat():
+    """SequenceLayout.unshard raises where the reference's torch.cat of the pieces raises
+    (other dimensions differ: RuntimeError) and promotes mixed dtypes as torch.cat does
+    (partition.py:235-244)."""
+    lay = cea.SequenceLayout(7, 2, [4, 3], "zigzag")
+    x = torch.arange(2 * 7 * 3, dtype=torch.float32).view(2, 7, 3)
+    a, b = lay.shard(x, 0), lay.shard(x, 1)
+    assert torch.equal(lay.unshard([a, b]), x)
+    mixed = lay.unshard([a, b.double()])
+    assert mixed.dtype == torch.float64 and torch.equal(mixed, x.double())
+    with pytest.raises(RuntimeError):
+        lay.unshard([a, b[:1]])
+    with pytest.raises(RuntimeError):
+        lay.unshard([a, b[..., :2]])
+
+
+def test_fused_column_parallel_layout_and_load():
+    """FusedColumnParallelLinear (tensor_parallel.py:264-313): the local slices stacked in part
+    order, loaded from full parameters; bad ranges and missing biases are ValueErrors."""
+    layer = cea.FusedColumnParallelLinear(6, [(8, 2, 4), (5, 0, 5), (4, 3, 1)], None, bias=True)
+    assert layer.parts == [(8, 2, 4), (5, 0, 5), (4, 3, 1)]
+    assert layer.local_sizes == [4, 5, 1]
+    assert tuple(layer.weight.shape) == (10, 6) and tuple(layer.bias.shape) == (10,)
+    g = torch.Generator().manual_seed(0)
+    ws = [torch.randn(o, 6, generator=g) for o, _, _ in layer.parts]
+    bs = [torch.randn(o, generator=g) for o, _, _ in layer.parts]
+    layer.load_full(ws, bs)
+    assert torch.equal(layer.weight, torch.cat([ws[0][2:6], ws[1], ws[2][3:4]]))
+    assert torch.equal(layer.bias, torch.cat([bs[0][2:6], bs[1], bs[2][3:4]]))
+    with pytest.raises(ValueError):
+        layer.load_full(ws, None)
+    with pytest.raises(ValueError):
+        layer.load_full(ws[:2], bs[:2])
+    for bad in ([(4, 3, 2)], [(4, -1, 2)], [(4, 0, -1)]):
+        with pytest.raises(ValueError):
+            cea.FusedColumnParallelLinear(4, bad)

@@ -112,3 +112,38 @@ def test_noalloc_refuses_oversized_calls(cea, dev):
     assert "static scratch" in cea._native.last_error()
     torch.cuda.synchronize()
     assert bool((out == 0).all()) and bool((lse == 0).all())
+
+
+def test_noalloc_takes_f32_decode_shapes(cea, dev):
+    """A float32 call of a decode shape needs no split-KV partials (that route is bf16 / f16
+    only): the no-allocation entry runs it and matches the workspace entry exactly, twice in
+    a row, the second call smaller."""
+    nat = cea._native
+    lib = nat.load_library()
+    for shape in ((4, 1, 9000, 32, 8, 128), (2, 1, 3000, 32, 8, 128)):
+        B, Sq, Sk, Hq, Hkv, D = shape
+        t = tuple(x.to(dev) for x in _inputs(B, Sq, Sk, Hq, Hkv, D, seed=B, decode=True))
+        t = (t[0].float(), t[1].float(), t[2].float(), t[3], t[4])
+        assert lib.cea_attention_workspace_bytes(B, Sq, Hq, Sk, Hkv, D, 0) <= SCRATCH_BYTES
+        res = []
+        for fn in ("cea_attention_with_lse", "cea_attention_with_lse_noalloc"):
+            out = torch.full((B, Sq, Hq, D), float("nan"), device=dev)
+            lse = torch.full((B, Hq, Sq), float("nan"), device=dev)
+            args = [nat.tensor_arg(x) for x in t]
+            o, l = nat.tensor_arg(out), nat.tensor_arg(lse)
+            stream = nat.stream_of(dev)
+            print(f"no-alloc test: {fn} f32 shape={shape}", flush=True)
+            if fn == "cea_attention_with_lse":
+                need = lib.cea_attention_workspace_bytes(B, Sq, Hq, Sk, Hkv, D, 0)
+                ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+                rc = lib.cea_attention_with_lse(*(byref(a) for a in args), 1, D ** -0.5, None, 0,
+                                                byref(o), byref(l), 0, ws.data_ptr(), ws.numel(), stream)
+            else:
+                rc = lib.cea_attention_with_lse_noalloc(*(byref(a) for a in args), 1, D ** -0.5, None,
+                                                        0, byref(o), byref(l), 0, stream)
+            assert rc == 0, (fn, rc, nat.last_error())
+            torch.cuda.synchronize()
+            res.append((out.cpu(), lse.cpu()))
+        assert torch.isfinite(res[0][0]).all()
+        assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+
