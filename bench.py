@@ -149,8 +149,8 @@ def bench_ring(cea, torch, steps, warmup, dev):
     }
 
 
-def bench_decode(cea, torch, steps, warmup, dev):
-    w = cea.workloads.kv_decode(device=dev)
+def bench_decode(cea, torch, steps, warmup, dev, hq=32, hkv=8, d=128):
+    w = cea.workloads.kv_decode(device=dev, hq=hq, hkv=hkv, d=d)
     parts = w.partitions()
     comm = cea.LocalGroup(len(parts), 0)
     for r, (k, v, p) in enumerate(parts):
@@ -167,7 +167,7 @@ def bench_decode(cea, torch, steps, warmup, dev):
     return {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
             "ms_per_step": round(gpu_ms, 4), "wall_ms_per_step": round(sec * 1e3, 4),
             "bytes": w.bytes,
-            "workload": "distributed-KV decode B=32 1 token 32/8 heads D=128 bf16, cache 32768, "
+            "workload": f"distributed-KV decode B=32 1 token {hq}/{hkv} heads D={d} bf16, cache 32768, "
                         "lengths U[1024,32768], 4 partitions 0.4/0.3/0.2/0.1 + exact merge"}
 
 
@@ -567,6 +567,9 @@ def main() -> int:
     if want("decode"):
         _log("distributed-KV decode")
         secondary["kv_decode"] = bench_decode(cea, torch, args.steps, args.warmup, dev)
+        # the same step at the tinyllama-1.1b preset's heads (32 query / 4 KV, head size 64)
+        secondary["kv_decode_d64"] = bench_decode(cea, torch, args.steps, args.warmup, dev,
+                                                  hq=32, hkv=4, d=64)
     if want("layers"):
         _log("layer ops")
         secondary["layer_ops"] = bench_layers(cea, torch, args.steps, args.warmup, dev)

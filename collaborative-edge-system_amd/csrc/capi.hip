@@ -467,7 +467,8 @@ static int ring_plan(RingPlan* rp, const cea_tensor* q, int32_t n, const cea_ten
   rp->fused = rp->first >= 0 && same_rows && tiles < ((int64_t)1 << 24) &&
               prefill_segs_supported(rp->p, rp->segs);
   if (rp->fused) {
-    rp->bytes = tile_bytes(rp->p.B, tiles);
+    // one summary per tile of every block and batch row (tile_bytes takes a key count)
+    rp->bytes = align_up((size_t)rp->p.B * (size_t)tiles * sizeof(TileInfo), 256);
   } else {
     // running (out, lse) in the accumulation dtype unless the caller's pair is that already
     const size_t esz = rp->p.in_dtype == CEA_F64 ? 8 : 4;

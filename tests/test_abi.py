@@ -232,3 +232,39 @@ def test_workspace_counts_decode_partials_only_for_the_decode_route(cea):
     assert f32 == f64 == odd == tiles
     # head size 64 takes the decode route as well
     assert lib.cea_attention_workspace_bytes(B, 1, Hq, Sk, Hkv, 64, 1) > tiles
+
+
+def _desc(nat, shape, dtype_code, addr):
+    """A contiguous cea_tensor over a fake (aligned, never dereferenced) device address."""
+    t = nat.CeaTensor()
+    t.data = addr
+    t.dtype = dtype_code
+    t.ndim = len(shape)
+    stride = 1
+    for i in reversed(range(len(shape))):
+        t.size[i] = shape[i]
+        t.stride[i] = stride
+        stride *= shape[i]
+    return t
+
+
+@pytest.mark.parametrize("B,sizes", [(1, [8192, 8192, 8192, 8192]), (3, [100, 65, 0, 300])])
+def test_ring_workspace_covers_every_tile_summary(cea, B, sizes):
+    """cea_ring_attention_workspace_bytes for the one-launch route: one 32-byte summary per
+    64-key tile of every block and batch row (a workspace sized for the tile count read as a
+    key count let the summary pass write past the buffer)."""
+    nat = cea._native
+    lib = nat.load_library()
+    Sq, Hq, Hkv, D = 512, 8, 2, 128
+    addr = iter(range(1 << 30, 1 << 40, 1 << 30))
+    q = _desc(nat, (B, Sq, Hq, D), 1, next(addr))
+    qp = _desc(nat, (B, Sq), 4, next(addr))
+    out = _desc(nat, (B, Sq, Hq, D), 1, next(addr))
+    n = len(sizes)
+    ks = (nat.CeaTensor * n)(*[_desc(nat, (B, s, Hkv, D), 1, next(addr)) for s in sizes])
+    vs = (nat.CeaTensor * n)(*[_desc(nat, (B, s, Hkv, D), 1, next(addr)) for s in sizes])
+    ps = (nat.CeaTensor * n)(*[_desc(nat, (B, s), 4, next(addr)) for s in sizes])
+    got = lib.cea_ring_attention_workspace_bytes(ctypes.byref(q), n, ks, vs, ctypes.byref(qp), ps, 1,
+                                                 None, 0, ctypes.byref(out), None)
+    tiles = sum((s + 63) // 64 for s in sizes)
+    assert got >= B * tiles * 32, (got, B * tiles * 32)
