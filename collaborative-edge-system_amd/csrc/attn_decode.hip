@@ -701,11 +701,16 @@ bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dt
   return Hq <= CEA_MAX_MAPPED_HEADS && decode_rows(Sq, 1) != 0;
 }
 
-int decode_plan_chunk(int64_t keys_per_head, int32_t B, int32_t units) {
-  // enough work items to fill 256 CUs several times, chunks of 256..1024 keys
+// Work items wanted per launch: enough to fill 256 CUs several times.  An item's bytes per key
+// scale with the head size, so the count scales with it too (a head size of 64 takes half as
+// many, twice the keys each: the same bytes per item as at 128).
+static int64_t decode_item_target(int32_t D) { return (int64_t)CEA_DECODE_ITEMS * D / 128; }
+
+int decode_plan_chunk(int64_t keys_per_head, int32_t B, int32_t units, int32_t D) {
+  // chunks of 256..1024 keys
   const int64_t heads = (int64_t)B * units;
   int ch = 256;
-  while (ch < CHMAX && heads * ((keys_per_head + ch - 1) / ch) > CEA_DECODE_ITEMS) ch *= 2;
+  while (ch < CHMAX && heads * ((keys_per_head + ch - 1) / ch) > decode_item_target(D)) ch *= 2;
   return ch;
 }
 
@@ -723,7 +728,7 @@ int launch_attn_decode(const DecodeParams& params, hipStream_t st) {
   for (int i = 0; i < p.nparts; ++i)
     p.item_begin[i + 1] = p.item_begin[i] + (p.chunk_begin[i + 1] - p.chunk_begin[i] + 1) / 2;
   const int64_t row_items = (int64_t)p.units * p.chunk_begin[p.nparts];
-  const bool pairs = p.chunk == CHMAX && p.B * row_items >= CEA_DECODE_ITEMS;
+  const bool pairs = p.chunk == CHMAX && p.B * row_items >= decode_item_target(p.D);
   const int cus = device_cus();
   const int64_t tail_rows = row_items > 0 ? (4 * (int64_t)(cus > 0 ? cus : 256) + row_items - 1) / row_items : 1;
   p.pair_rows = pairs ? (int)max((int64_t)0, (int64_t)p.B - tail_rows) : 0;

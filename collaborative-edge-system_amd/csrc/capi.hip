@@ -168,7 +168,7 @@ static DecodePlan plan_decode(const int64_t* Sk, int n, int64_t B, int64_t Sq, i
   DecodePlan pl;
   int64_t keys = 0;
   for (int i = 0; i < n; ++i) keys += Sk[i];
-  pl.chunk = decode_plan_chunk(keys, (int32_t)B, (int32_t)units);
+  pl.chunk = decode_plan_chunk(keys, (int32_t)B, (int32_t)units, (int32_t)D);
   pl.total_chunks = 0;
   for (int i = 0; i < n; ++i) pl.total_chunks += (int)((Sk[i] + pl.chunk - 1) / pl.chunk);
   pl.nr = decode_rows((int32_t)Sq, (int32_t)G);
