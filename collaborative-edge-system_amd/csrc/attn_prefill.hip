@@ -237,13 +237,26 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   struct TileSrc {
     i32x4 krs, vrs, prs;
   };
+  // With several blocks the list runs block by block, so the bases of the block whose tiles
+  // are being loaded are kept and recomputed only when the block changes.
+  int src_seg = -1, src_sk = 0;
+  const char *src_k = nullptr, *src_v = nullptr, *src_p = nullptr;
+  int cur_seg = -1, cur_sk = 0;  // the same for the block of the tile being computed
   auto tile_src = [&](int x) {
-    const KvSeg& sg = seg_of(x);
+    const int si = MULTI ? (x >> 24) : 0;
+    if (!MULTI || si != src_seg) {
+      const KvSeg& sg = segs.seg[si];
+      src_k = (const char*)((const T*)sg.k + b * sg.ks_b + kvh * sg.ks_h);
+      src_v = (const char*)((const T*)sg.v + b * sg.vs_b + kvh * sg.vs_h);
+      src_p = (const char*)(sg.k_pos + b * sg.kps_b);
+      src_sk = sg.Sk;
+      src_seg = si;
+    }
     const int key0 = (x & 0xffffff) * BN;
-    const int left = sg.Sk - key0;  // > 0 for every listed tile
-    const char* kbase = (const char*)((const T*)sg.k + b * sg.ks_b + kvh * sg.ks_h);
-    const char* vbase = (const char*)((const T*)sg.v + b * sg.vs_b + kvh * sg.vs_h);
-    const char* pbase = (const char*)(sg.k_pos + b * sg.kps_b);
+    const int left = src_sk - key0;  // > 0 for every listed tile
+    const char* kbase = src_k;
+    const char* vbase = src_v;
+    const char* pbase = src_p;
     TileSrc ts;
     ts.krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, (uint32_t)(left - 1) * krow_bytes + L::KROW);
     ts.vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, (uint32_t)(left - 1) * vrow_bytes + L::KROW);
@@ -424,7 +437,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     if (n == 0) continue;
     int issued = 0;
     for (; issued < n && issued < NSTAGE - 1; ++issued)
-      load_tile(tile_src(__builtin_amdgcn_readfirstlane(tile_list[issued].x)), issued % NSTAGE);
+      load_tile(tile_src(__builtin_amdgcn_readfirstlane(tile_list[issued].x)), (int)((unsigned)issued % NSTAGE));
     // The list entries of the next step (its tile and this wave's mode, and the tile to load
     // after it) are read from LDS right after the barrier and only used after this step's
     // work, so their latency hides under it; so does the kernel-argument read of the tile's
@@ -438,13 +451,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
       else wait_tiles_ahead<L::LOADS_PER_TILE>(issued - i - 1);
       barrier_no_fence();  // tile i landed for every wave; the stage of tile i-1 is free
       if (issued < n) {
-        load_tile(tile_src(x_load), issued % NSTAGE);
+        load_tile(tile_src(x_load), (int)((unsigned)issued % NSTAGE));
         ++issued;
       }
-      const int left_cur = seg_of(x_cur).Sk - (x_cur & 0xffffff) * BN;
+      if (MULTI && (x_cur >> 24) != cur_seg) {
+        cur_seg = x_cur >> 24;
+        cur_sk = segs.seg[cur_seg].Sk;
+      }
+      const int left_cur = (MULTI ? cur_sk : segs.seg[0].Sk) - (x_cur & 0xffffff) * BN;
       const int2 e_nxt = tile_list[i + 1 < n ? i + 1 : i];
       const int xl_nxt = tile_list[issued < n ? issued : 0].x;
-      if (m_cur != 0) compute(i % NSTAGE, left_cur, m_cur);
+      if (m_cur != 0) compute((int)((unsigned)i % NSTAGE), left_cur, m_cur);
       x_cur = __builtin_amdgcn_readfirstlane(e_nxt.x);
       m_cur = __builtin_amdgcn_readfirstlane((e_nxt.y >> mshift) & 3);
       x_load = __builtin_amdgcn_readfirstlane(xl_nxt);
