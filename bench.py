@@ -397,8 +397,8 @@ def cpu_baseline(cea, torch):
     from oracle import layers_ref as lref
     from oracle import sp_ref
 
-    # the process's CPU share: OMP_NUM_THREADS where the host sets it (the GPU box gives each
-    # GPU 16 cores), else every core this process may run on
+    # the process's CPU share: OMP_NUM_THREADS where the host sets it (a host shared by several
+    # GPUs may give each its own set of cores), else every core this process may run on
     try:
         avail = len(os.sched_getaffinity(0))
     except (AttributeError, OSError):
@@ -549,7 +549,7 @@ def main() -> int:
                           "gbs": round(2 * n * 4 / sec / 1e9, 1)}), flush=True)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build simulates every rank's share on a single "
+        print("bench.py measures one GPU: this package simulates every rank's share on a single "
               "MI355X and has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
     import torch

@@ -1,16 +1,19 @@
 """One rank's share of ring attention, Ulysses attention and distributed-KV decoding, run on
 one GPU.
 
-Drop-in signatures of collab_infer/parallel/sequence_parallel.py.  The collectives are not
-part of this build: the ``comm`` argument is a :class:`LocalGroup` that already holds what
-the other simulated ranks would send (their KV blocks, partitions or token shards), so a
-rank's share is computed at its real shape by streaming those blocks through the kernels:
+Drop-in signatures of collab_infer/parallel/sequence_parallel.py.  This package runs no
+collectives: the ``comm`` argument is a :class:`LocalGroup` that already holds what the other
+simulated ranks would send (their KV blocks, partitions or token shards), so a rank's share
+is computed at its real shape by streaming those blocks through the kernels:
 
 * :func:`ring_attention` (sequence_parallel.py:68-130) - the rank's queries against every
-  rank's KV block in ring order ``(r - step) mod n``, each block merged exactly into a
-  running ``(out, lse)`` in the attention kernel's epilogue.  Fully hidden blocks cost one
-  pass over their position summaries (the kernel skips their tiles), which replaces the
-  reference's host-side ``fully_masked`` test without a device-to-host sync.
+  rank's KV block in ring order ``(r - step) mod n``, merged exactly: one
+  ``cea_ring_attention`` call whose single prefill launch carries each query row's softmax
+  state across the blocks, or, where one launch does not fit, block after block with each
+  block merged into a running ``(out, lse)`` in the attention kernel's epilogue.  Fully
+  hidden blocks cost one pass over their position summaries (the kernel skips their tiles),
+  which replaces the reference's host-side ``fully_masked`` test without a device-to-host
+  sync.
 * :func:`distributed_kv_attention` (sequence_parallel.py:250-280) - a replicated query
   against every rank's cache partition, partials merged exactly (``merge_attention_list``).
 * :func:`ulysses_scatter` / :func:`ulysses_gather` / :func:`ulysses_attention`

@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY.  This package restates, on the CPU and in PyTorch's CPU
 operators, the algorithm the reference implements for this path, so the gfx950 kernels can
 be checked against it.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker / the timed CPU
-baseline; the product package never imports, calls or falls back to it.
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the reference results to
+compare with / the timed CPU baseline; the product package never imports, calls or falls back to it.
 
 Modules:
 * :mod:`oracle.attention_ref` - attention_with_lse / attention / merges
