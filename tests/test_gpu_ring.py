@@ -131,3 +131,26 @@ def test_ring_share_nothing_visible(cea, dev):
     q_pos = blocks[rank][2]
     out, lse, plain = _run(cea, dev, q, q_pos, pad_blocks, rank)
     assert not plain.cpu().any() and (lse.cpu() == float("-inf")).all()
+
+
+def test_ring_share_batch_of_two(cea, dev):
+    """Two batch rows with different padding in every block (the tile summaries are per batch
+    row): the one-call share against the oracle's ring loop."""
+    g = torch.Generator().manual_seed(21)
+    sizes, hq, hkv, d = [260, 200, 130], 4, 2, 128
+    blocks, start = [], 0
+    for n in sizes:
+        k = torch.randn(2, n, hkv, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(2, n, hkv, d, generator=g).to(torch.bfloat16)
+        pos = torch.arange(start, start + n).repeat(2, 1)
+        pos[1, n // 3:] = -1  # the second row is padded from a third of each block on
+        blocks.append((k, v, pos))
+        start += n
+    rank = 1
+    q = torch.randn(2, sizes[rank], hq, d, generator=g).to(torch.bfloat16)
+    q_pos = blocks[rank][2].clone()
+    q_pos[1] = torch.arange(sizes[0], sizes[0] + sizes[rank])
+    out, lse, plain = _run(cea, dev, q, q_pos, blocks, rank)
+    ro, rl = sp_ref.ring_share(q, q_pos, blocks, rank, with_lse=True)
+    assert_attention_close(out, lse, ro, rl, torch.bfloat16, "ring share, two batch rows")
+    assert torch.equal(plain.cpu(), out.to(torch.bfloat16).cpu())

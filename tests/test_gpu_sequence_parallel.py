@@ -182,6 +182,41 @@ def test_partitioned_decode_matches_oracle(cea, dev, shape, dtype):
     assert_attention_close(o1, l1, r1, s1, dtype, "single partition")
 
 
+@pytest.mark.parametrize("d,kv_map", [(128, None), (64, None), (64, [1, 0, 0, 1, 1, 0])],
+                         ids=["d128", "d64", "d64-map"])
+def test_partitioned_decode_without_causal_rule(cea, dev, d, kv_map):
+    """causal=False with a negative scale on the split-KV decode path: every valid slot is
+    visible (k_pos >= 0 alone decides), including slots past the queries' own positions; each
+    partition's (out, lse), the merge and the q-dtype result against the oracle."""
+    g = torch.Generator().manual_seed(77 + d)
+    Bn, Sq, Hq, Hkv, cap, sizes = 3, 2, 6, 2, 900, [500, 250, 150]
+    dtype = torch.bfloat16
+    ck = torch.randn(Bn, Hkv, cap, d, generator=g).to(dtype)
+    cv = torch.randn(Bn, Hkv, cap, d, generator=g).to(dtype)
+    q = torch.randn(Bn, Sq, Hq, d, generator=g).to(dtype)
+    lens = torch.tensor([900, 321, 17])
+    slots = torch.arange(cap).view(1, cap)
+    kpos = torch.where(slots < lens.view(-1, 1), slots, torch.full_like(slots, -1))
+    qpos = torch.tensor([[3, 4], [100, 101], [0, 1]])  # before most of the valid slots
+    parts, parts_cpu, start = [], [], 0
+    for n in sizes:
+        sl = slice(start, start + n)
+        parts_cpu.append((ck[:, :, sl].transpose(1, 2), cv[:, :, sl].transpose(1, 2), kpos[:, sl]))
+        parts.append(tuple(t.to(dev) for t in parts_cpu[-1]))
+        start += n
+    kw = dict(causal=False, scale=-0.07, kv_map=kv_map)
+    out, lse, per = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts, return_lse=True,
+                                              return_parts=True, **kw)
+    out_q = cea.partitioned_attention(q.to(dev), qpos.to(dev), parts, **kw)
+    torch.cuda.synchronize()
+    ro, rl, rparts = sp_ref.distributed_kv_share(q, qpos, parts_cpu, with_parts=True, **kw)
+    for i, ((po, pl), (qo, ql)) in enumerate(zip(per, rparts)):
+        assert_attention_close(po, pl, qo, ql, dtype, f"partition {i}")
+    assert_attention_close(out, lse, ro.float(), rl, dtype, "merged")
+    assert out_q.dtype == dtype
+    assert (out_q.cpu().float() - ro.float()).abs().max().item() <= 2e-2
+
+
 def test_kv_decode_workload_subset_matches_oracle(cea, dev):
     """Four sequences of the distributed-KV decode workload (cache 32768, 4 partitions)
     through distributed_kv_attention on simulated ranks vs the oracle."""
