@@ -154,3 +154,35 @@ def test_ring_share_batch_of_two(cea, dev):
     ro, rl = sp_ref.ring_share(q, q_pos, blocks, rank, with_lse=True)
     assert_attention_close(out, lse, ro, rl, torch.bfloat16, "ring share, two batch rows")
     assert torch.equal(plain.cpu(), out.to(torch.bfloat16).cpu())
+
+
+@pytest.mark.parametrize("sizes", [[0, 0, 0], [0, 90, 0]], ids=["all-empty", "one-block"])
+def test_ring_share_empty_blocks(cea, dev, sizes):
+    """Ranks holding no keys: with no key anywhere the share is the merge's neutral element
+    (zeros, lse -inf); with one non-empty block it is that block's attention."""
+    g = torch.Generator().manual_seed(31)
+    hq, hkv, d = 4, 2, 128
+    blocks, start = [], 0
+    for n in sizes:
+        blocks.append((torch.randn(1, n, hkv, d, generator=g).to(torch.bfloat16),
+                       torch.randn(1, n, hkv, d, generator=g).to(torch.bfloat16),
+                       torch.arange(start, start + n).view(1, n)))
+        start += n
+    q = torch.randn(1, 50, hq, d, generator=g).to(torch.bfloat16)
+    q_pos = torch.arange(40, 90).view(1, 50)
+    out, lse, plain = _run(cea, dev, q, q_pos, blocks, 1)
+    assert torch.equal(plain.cpu(), out.to(torch.bfloat16).cpu())
+    ro, rl = sp_ref.ring_share(q, q_pos, blocks, 1, with_lse=True)
+    if rl is None:  # the reference skips every block and returns zeros (no lse)
+        assert not out.cpu().any() and (lse.cpu() == float("-inf")).all()
+        assert not ro.any()
+    else:
+        assert_attention_close(out, lse, ro, rl, torch.bfloat16, f"ring share {sizes}")
+
+
+def test_ring_share_no_queries(cea, dev):
+    """A rank with no query tokens returns empty results of the right shapes."""
+    q, q_pos, blocks, rank = _share(3, [100, 120, 80], 4, 2, 64, seed=5)
+    q, q_pos = q[:, :0], q_pos[:, :0]
+    out, lse, plain = _run(cea, dev, q, q_pos, blocks, rank)
+    assert out.shape == (1, 0, 4, 64) and lse.shape == (1, 4, 0) and plain.shape == (1, 0, 4, 64)
