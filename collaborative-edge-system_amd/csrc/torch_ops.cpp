@@ -83,6 +83,13 @@ at::Device device_of(std::initializer_list<const Tensor*> ts, at::TensorList mor
   return *dev;
 }
 
+// Every tensor of a further list on the device `dev` found for the call's other tensors.
+void on_device(const at::Device& dev, at::TensorList more) {
+  if (more.empty()) return;
+  const at::Device d = device_of({}, more);
+  TORCH_CHECK(d == dev, "tensors on different devices: ", dev, " and ", d);
+}
+
 void* stream_of(const at::Device& d) {
   return (void*)c10::hip::getCurrentHIPStream(d.index()).stream();
 }
@@ -199,7 +206,7 @@ std::vector<Tensor> merge(at::TensorList outs_in, at::TensorList lses, bool pair
   TORCH_CHECK_VALUE(!outs_in.empty() && outs_in.size() == lses.size(),
                     "need the same positive number of outputs and lses");
   const at::Device dev = device_of({}, outs_in);
-  device_of({}, lses);
+  on_device(dev, lses);
   std::vector<Tensor> outs;
   for (const Tensor& o : outs_in) outs.push_back(inner(o));
   const Tensor& o0 = outs[0];
@@ -224,8 +231,8 @@ std::vector<Tensor> partitioned(const Tensor& q_in, const Tensor& q_pos_in, at::
   TORCH_CHECK_VALUE(n >= 1 && (int64_t)vs_in.size() == n && (int64_t)ps_in.size() == n,
                     "need one k, v and position tensor per partition");
   const at::Device dev = device_of({&q_in, &q_pos_in}, ks_in);
-  device_of({}, vs_in);
-  device_of({}, ps_in);
+  on_device(dev, vs_in);
+  on_device(dev, ps_in);
   const Tensor q = inner(q_in), qp = as_i64(q_pos_in);
   std::vector<Tensor> ks, vs, ps;
   for (int64_t i = 0; i < n; ++i) {
@@ -277,8 +284,8 @@ std::vector<Tensor> ring(const Tensor& q_in, const Tensor& q_pos_in, at::TensorL
   TORCH_CHECK_VALUE(n >= 1 && (int64_t)vs_in.size() == n && (int64_t)ps_in.size() == n,
                     "need one k, v and position tensor per KV block");
   const at::Device dev = device_of({&q_in, &q_pos_in}, ks_in);
-  device_of({}, vs_in);
-  device_of({}, ps_in);
+  on_device(dev, vs_in);
+  on_device(dev, ps_in);
   const Tensor q = inner(q_in), qp = as_i64(q_pos_in);
   TORCH_CHECK_VALUE(q.dim() == 4, "q must be [B, S, H, D]");
   std::vector<Tensor> ks, vs, ps;
@@ -346,9 +353,9 @@ std::vector<Tensor> ulysses_scatter(at::TensorList qs, at::TensorList ks, at::Te
   TORCH_CHECK_VALUE(n >= 1 && (int64_t)ks.size() == n && (int64_t)vs.size() == n && (int64_t)ps.size() == n,
                     "need one q, k, v and position shard per rank");
   const at::Device dev = device_of({}, qs);
-  device_of({}, ks);
-  device_of({}, vs);
-  device_of({}, ps);
+  on_device(dev, ks);
+  on_device(dev, vs);
+  on_device(dev, ps);
   std::vector<Tensor> pl;
   for (const Tensor& p : ps) pl.push_back(as_i64(p));
   int64_t S = 0;

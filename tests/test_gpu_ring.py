@@ -186,3 +186,16 @@ def test_ring_share_no_queries(cea, dev):
     q, q_pos = q[:, :0], q_pos[:, :0]
     out, lse, plain = _run(cea, dev, q, q_pos, blocks, rank)
     assert out.shape == (1, 0, 4, 64) and lse.shape == (1, 4, 0) and plain.shape == (1, 0, 4, 64)
+
+
+def test_ring_share_rejects_a_block_off_the_device(cea, dev):
+    """Every tensor of a call must live on the queries' device: a value block left on the
+    host raises before any kernel runs."""
+    q, q_pos, blocks, rank = _share(3, [100, 120, 80], 4, 2, 64, seed=9)
+    grp = _group(cea, dev, 3, rank, blocks)
+    k2, v2, p2 = blocks[2]
+    grp.set_shard(2, k=k2.to(dev), v=v2, pos=p2.to(dev))  # v stays on the host
+    own = grp.shard(rank)
+    with pytest.raises(RuntimeError):
+        cea.ring_attention(q.to(dev), own["k"], own["v"], q_pos.to(dev), own["pos"], grp,
+                           [100, 120, 80])
