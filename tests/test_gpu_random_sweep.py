@@ -4,7 +4,9 @@ Combinations the hand-picked cases do not pin one by one: batch, query and key c
 (partial tiles, one-row blocks), head counts with regular and irregular kv maps, head sizes
 of the matrix-core, f32 and generic kernels, every mask pattern of tests/_cases.py, causal
 and not, default / negative / small scales, kv_block splits, and partitioned (distributed-KV)
-calls with 1 to 5 partitions of random sizes through the split-KV decode route.  The cases
+calls with 1 to 5 partitions of random sizes through the split-KV decode route, and ring
+shares over 2 to 5 simulated ranks through the one-call route (empty and tiny blocks,
+padding, two batch rows, head sizes 64 and 128, regular and irregular maps).  The cases
 are drawn from a fixed seed, so a run is reproducible; tolerances are those of
 tests/_cases.py.
 """
@@ -163,3 +165,64 @@ def test_partitions_with_empty_ranks(cea, dev, sizes):
     assert_attention_close(out, lse, ro, rl, dtype, "merged")
     if start == 0:
         assert bool((out == 0).all()) and bool(torch.isinf(lse).all())
+
+
+def _ring_cases(n=40, seed=4242):
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        world = rng.choice([2, 3, 4, 5])
+        sizes = [rng.choice([0, rng.randrange(1, 80), rng.randrange(64, 700)]) for _ in range(world)]
+        rank = rng.randrange(world)
+        if sizes[rank] == 0:
+            sizes[rank] = rng.randrange(1, 300)
+        hkv = rng.choice([1, 2, 4])
+        hq = hkv * rng.choice([1, 2, 3, 4])
+        kv_map = None
+        if rng.random() < 0.25:
+            heads = list(range(hkv)) + [rng.randrange(hkv) for _ in range(hq - hkv)]
+            kv_map = tuple(sorted(heads))
+        causal = rng.random() < 0.7
+        # non-positive scales only without the causal rule (the CPU flash operator returns
+        # NaN for is_causal with scale <= 0)
+        scale = rng.choice([None, None, 0.05] + ([] if causal else [-0.1]))
+        cases.append((i, world, rank, rng.choice([1, 1, 2]), sizes, hq, hkv, rng.choice([64, 128]),
+                      rng.choice([torch.bfloat16, torch.float16]), causal, kv_map, scale,
+                      rng.random() < 0.3))
+    return cases
+
+
+@pytest.mark.parametrize("rc", _ring_cases(), ids=lambda c: f"r{c[0]}-w{c[1]}-{c[4]}")
+def test_random_ring_shares_match_oracle(cea, dev, rc):
+    """One rank's ring share in one call (cea_ring_attention) against the oracle's ring loop:
+    (out, lse) and the q-dtype result (the f32 result rounded once)."""
+    i, world, rank, B, sizes, hq, hkv, d, dtype, causal, kv_map, scale, padded = rc
+    g = torch.Generator().manual_seed(5000 + i)
+    blocks, start = [], 0
+    for n in sizes:
+        k = torch.randn(B, n, hkv, d, generator=g).to(dtype)
+        v = torch.randn(B, n, hkv, d, generator=g).to(dtype)
+        pos = torch.arange(start, start + n).repeat(B, 1)
+        if padded and n:
+            pos[torch.rand(B, n, generator=g) < 0.2] = -1
+        blocks.append((k, v, pos))
+        start += n
+    q = torch.randn(B, sizes[rank], hq, d, generator=g).to(dtype)
+    q_pos = blocks[rank][2].clone()
+    print(f"ring w{world} r{rank} B{B} {sizes} h{hq}/{hkv} d{d} {dtype} causal={causal} "
+          f"map={kv_map} scale={scale}", flush=True)
+    grp = cea.LocalGroup(world, rank)
+    for r, (k, v, p) in enumerate(blocks):
+        grp.set_shard(r, k=k.to(dev), v=v.to(dev), pos=p.to(dev))
+    own = grp.shard(rank)
+    kw = dict(causal=causal, scale=scale, kv_map=kv_map)
+    out, lse = cea.sequence_parallel.ring_attention_with_lse(q.to(dev), own["k"], own["v"],
+                                                             q_pos.to(dev), own["pos"], grp, sizes, **kw)
+    plain = cea.ring_attention(q.to(dev), own["k"], own["v"], q_pos.to(dev), own["pos"], grp, sizes, **kw)
+    torch.cuda.synchronize()
+    ro, rl = sp_ref.ring_share(q, q_pos, blocks, rank, with_lse=True, **kw)
+    if rl is None:  # no block visible to any query: zeros (the reference returns no lse)
+        assert not out.cpu().any() and (lse.cpu() == float("-inf")).all()
+    else:
+        assert_attention_close(out, lse, ro, rl, dtype, "ring share")
+    assert torch.equal(plain.cpu(), out.to(dtype).cpu())
