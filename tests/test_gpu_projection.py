@@ -262,5 +262,10 @@ def test_fused_qkv_projection_views_feed_the_kernels(cea, dev):
     pos = torch.arange(S, device=dev).repeat(B, 1)
     out = cea.attention_fn(q4, k4, v4, pos, pos)
     ref = cea.attention_fn(q4.contiguous(), k4.contiguous(), v4.contiguous(), pos, pos)
+    # a decode-shaped call (the last two tokens' queries: the split-KV route) on the views
+    dq, dqp = q4[:, -2:], pos[:, -2:]
+    dout, dlse = cea.attention_with_lse(dq, k4, v4, dqp, pos)
+    dref, dlref = cea.attention_with_lse(dq.contiguous(), k4.contiguous(), v4.contiguous(), dqp, pos)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+    assert torch.equal(dout, dref) and torch.equal(dlse, dlref)
