@@ -470,7 +470,7 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
 //      the same sums restricted to a partition, times exp(lse - lse_p).
 constexpr int RTHREADS = 256;
 constexpr int RWAVES = RTHREADS / 64;
-constexpr int RCH = kDecodeMaxChunks;  // chunks staged per row
+constexpr int RCH = kDecodeMaxChunks;  // work items of a row at most (m and weight in LDS)
 constexpr int RPF = 12;                // chunk outputs per wave read ahead of their weights
 
 // Output features per lane: D / 64 consecutive floats (a float2 for D = 128, one float for 64).
@@ -510,8 +510,10 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   const int64_t cstride = (int64_t)NR * (D + 2);
   const float* base = p.partial + ((int64_t)b * p.units + unit) * total_chunks * cstride + r * (D + 2);
 
-  __shared__ float m_s[RCH];
-  __shared__ float w_s[RCH];
+  // m of every item of the row, then its weight: 2 x total_chunks floats of dynamic LDS
+  extern __shared__ float stage_s[];
+  float* m_s = stage_s;
+  float* w_s = stage_s + total_chunks;
   __shared__ V acc_s[RWAVES][64];
 
   // the first chunk outputs of this wave, read now so their latency overlaps the statistics
@@ -661,12 +663,23 @@ int launch_nr(const DecodeParams& p, hipStream_t st) {
   }
   const int rows = p.B * p.Sq * p.Hq;
   if (rows == 0) return CEA_OK;
-  if (p.out_dtype == CEA_F32)
-    hipLaunchKernelGGL((decode_reduce_kernel<float, D, NR>), dim3(rows), dim3(RTHREADS), 0, st, p);
-  else if (p.out_dtype == CEA_BF16)
-    hipLaunchKernelGGL((decode_reduce_kernel<bf16, D, NR>), dim3(rows), dim3(RTHREADS), 0, st, p);
-  else
-    hipLaunchKernelGGL((decode_reduce_kernel<f16, D, NR>), dim3(rows), dim3(RTHREADS), 0, st, p);
+  const int stage = 2 * total * (int)sizeof(float);
+  hipError_t e;
+  if (p.out_dtype == CEA_F32) {
+    e = reserve_lds<decode_reduce_kernel<float, D, NR>>(2 * RCH * (int)sizeof(float));
+    if (e == hipSuccess)
+      hipLaunchKernelGGL((decode_reduce_kernel<float, D, NR>), dim3(rows), dim3(RTHREADS), stage, st, p);
+  } else if (p.out_dtype == CEA_BF16) {
+    e = reserve_lds<decode_reduce_kernel<bf16, D, NR>>(2 * RCH * (int)sizeof(float));
+    if (e == hipSuccess)
+      hipLaunchKernelGGL((decode_reduce_kernel<bf16, D, NR>), dim3(rows), dim3(RTHREADS), stage, st, p);
+  } else {
+    e = reserve_lds<decode_reduce_kernel<f16, D, NR>>(2 * RCH * (int)sizeof(float));
+    if (e == hipSuccess)
+      hipLaunchKernelGGL((decode_reduce_kernel<f16, D, NR>), dim3(rows), dim3(RTHREADS), stage, st, p);
+  }
+  CEA_REQUIRE(e == hipSuccess, CEA_ELAUNCH, "decode: cannot reserve %d bytes of LDS: %s",
+              2 * RCH * (int)sizeof(float), hipGetErrorString(e));
   CEA_CHECK_LAUNCH("decode_reduce");
   return CEA_OK;
 }

@@ -253,14 +253,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
       src_seg = si;
     }
     const int key0 = (x & 0xffffff) * BN;
-    const int left = src_sk - key0;  // > 0 for every listed tile
+    // keys of the tile that exist (> 0 for every listed tile); the resources span those rows
+    // only, so their ranges stay 32-bit however large the block is
+    const int rows = min(src_sk - key0, BN);
     const char* kbase = src_k;
     const char* vbase = src_v;
     const char* pbase = src_p;
     TileSrc ts;
-    ts.krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, (uint32_t)(left - 1) * krow_bytes + L::KROW);
-    ts.vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, (uint32_t)(left - 1) * vrow_bytes + L::KROW);
-    ts.prs = make_rsrc(pbase + (int64_t)key0 * 8, (uint32_t)left * 8);
+    ts.krs = make_rsrc(kbase + (int64_t)key0 * krow_bytes, (uint32_t)(rows - 1) * krow_bytes + L::KROW);
+    ts.vrs = make_rsrc(vbase + (int64_t)key0 * vrow_bytes, (uint32_t)(rows - 1) * vrow_bytes + L::KROW);
+    ts.prs = make_rsrc(pbase + (int64_t)key0 * 8, (uint32_t)rows * 8);
     return ts;
   };
   // this wave's share of a tile's loads: K rows, V rows and (16 lanes) key positions
@@ -618,11 +620,9 @@ static bool prefill_block_ok(const AttnParams& p, const KvSeg& g) {
   if (!al16(g.k) || !al16(g.v)) return false;
   // key positions are fetched 16 bytes at a time: contiguous, 16-byte aligned per batch
   if (g.kps_s != 1 || g.kps_b % 2 || !al16(g.k_pos)) return false;
-  // the block of one (batch, kv head) stays below 2 GiB
-  const int64_t kspan = ((int64_t)g.Sk - 1) * p.ks_s * 2 + p.D * 2;
-  const int64_t vspan = ((int64_t)g.Sk - 1) * p.vs_s * 2 + p.D * 2;
-  if (kspan >= ((int64_t)1 << 31) || vspan >= ((int64_t)1 << 31)) return false;
-  return true;
+  // tiles are addressed from 64-bit bases with 32-bit offsets inside one tile, so a block may
+  // span any number of bytes; list entries hold a tile of the block in 24 bits
+  return ((int64_t)g.Sk + kTileKeys - 1) / kTileKeys < ((int64_t)1 << 24);
 }
 
 bool prefill_mfma_supported(const AttnParams& p) {

@@ -204,7 +204,7 @@ bool f32_mfma_supported(const AttnParams& p);
 int launch_attn_f32_mfma(const AttnParams& p, hipStream_t s);
 bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dtype,
                       const HeadMap& map);
-constexpr int kDecodeMaxChunks = 1024;  // key chunks per (batch, kv head), all partitions
+constexpr int kDecodeMaxChunks = 16384;  // key chunks per (batch, kv head), all partitions
 int decode_plan_chunk(int64_t total_keys, int32_t B, int32_t units, int32_t D);
 int decode_rows(int32_t Sq, int32_t G);  // padded query rows per kv head, 0 = unsupported
 int launch_attn_decode(const DecodeParams& p, hipStream_t s);

@@ -273,3 +273,78 @@ def test_empty_query_or_key_block(cea, dev, Sq, Sk):
     assert out.shape == ro.shape and out.dtype == ro.dtype and lse.shape == rl.shape
     assert torch.equal(out.cpu(), ro) and torch.equal(lse.cpu(), rl)
     assert plain.shape == q.shape and plain.dtype == q.dtype and bool((plain == 0).all())
+
+
+def test_key_block_spanning_more_than_4gib(cea, dev):
+    """K and V as strided views whose rows are 1 MiB apart, so one (batch, KV head) block spans
+    more than 4 GiB: the matrix-core prefill kernel addresses every tile from a 64-bit base
+    with 32-bit offsets inside the tile, so the call is bit-identical to the same call on
+    contiguous copies (the route those take) and within the bf16 tolerances of the oracle;
+    the same for a decode-shaped call and for a one-launch ring share over two such blocks."""
+    g = torch.Generator().manual_seed(11)
+    B, Sq, Sk, hq, hkv, d = 1, 300, 4160, 4, 2, 128
+    row = 1 << 19  # elements per key row of the storage (1 MiB of bf16)
+    q = torch.randn(B, Sq, hq, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Sk, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Sk, hkv, d, generator=g).to(torch.bfloat16)
+    kp = torch.arange(Sk).view(1, Sk)
+    qp = torch.arange(Sk - Sq, Sk).view(1, Sq)
+    views = []
+    for t in (k, v):
+        store = torch.empty(Sk, row, dtype=torch.bfloat16, device=dev)
+        store[:, :hkv * d] = t.view(Sk, hkv * d).to(dev)
+        views.append(store[:, :hkv * d].view(1, Sk, hkv, d))
+    kv, vv = views
+    assert kv.stride(1) * 2 * (Sk - 1) > 1 << 32
+    qd, kd, vd, qpd, kpd = q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev)
+    out, lse = cea.attention_with_lse(qd, kv, vv, qpd, kpd)
+    ref_o, ref_l = cea.attention_with_lse(qd, kd, vd, qpd, kpd)
+    dout, dlse = cea.attention_with_lse(qd[:, -1:], kv, vv, qpd[:, -1:], kpd)
+    dref_o, dref_l = cea.attention_with_lse(qd[:, -1:], kd, vd, qpd[:, -1:], kpd)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_o) and torch.equal(lse, ref_l)
+    assert torch.equal(dout, dref_o) and torch.equal(dlse, dref_l)
+    ro, rl = ref.attention_with_lse(q, k, v, qp, kp)
+    assert_attention_close(out, lse, ro, rl, torch.bfloat16, "block beyond 4 GiB")
+    # a ring share over two blocks of the strided storage, in one launch
+    n = Sk // 2
+    sizes = [n, Sk - n]
+    results = []
+    for kk, vv_ in ((kv, vv), (kd, vd)):
+        comm = cea.LocalGroup(2, 1)
+        for r, (lo, hi) in enumerate(((0, n), (n, Sk))):
+            comm.set_shard(r, k=kk[:, lo:hi], v=vv_[:, lo:hi], pos=kpd[:, lo:hi])
+        own = comm.shard(1)
+        results.append(cea.sequence_parallel.ring_attention_with_lse(
+            qd, own["k"], own["v"], qpd, own["pos"], comm, sizes))
+    torch.cuda.synchronize()
+    assert torch.equal(results[0][0], results[1][0]) and torch.equal(results[0][1], results[1][1])
+    assert_attention_close(results[0][0], results[0][1], ro, rl, torch.bfloat16, "ring beyond 4 GiB")
+
+
+def test_decode_against_more_than_a_million_keys(cea, dev):
+    """A decode-shaped call against 1.2 M keys (2344 chunks of the split-KV kernels) and a
+    distributed-KV step over four partitions of 300 k keys each, both single split-KV
+    launches: against the oracle at the bf16 tolerances.  One key near the end of the range
+    is planted to dominate head 0's softmax, so a dropped chunk changes the output, not only
+    the lse."""
+    g = torch.Generator().manual_seed(12)
+    Sk, hq, hkv, d = 1_200_000, 4, 1, 64
+    q = torch.randn(1, 1, hq, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, Sk, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, Sk, hkv, d, generator=g).to(torch.bfloat16)
+    k[0, 1_100_000, 0] = 4 * q[0, 0, 0]
+    kp = torch.arange(Sk).view(1, Sk)
+    kp[0, -1000:] = -1
+    qp = torch.tensor([[Sk - 500]])
+    ro, rl = ref.attention_with_lse(q, k, v, qp, kp)
+    qd, kd, vd, qpd, kpd = q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev)
+    out, lse = cea.attention_with_lse(qd, kd, vd, qpd, kpd)
+    torch.cuda.synchronize()
+    assert ro[0, 0, 0].sub(v[0, 1_100_000, 0].double()).abs().max() < 1e-2  # the planted key rules
+    assert_attention_close(out, lse, ro, rl, torch.bfloat16, "decode over 1.2 M keys")
+    cuts = [0, 300_000, 600_000, 900_000, Sk]
+    parts = [(kd[:, a:b], vd[:, a:b], kpd[:, a:b]) for a, b in zip(cuts, cuts[1:])]
+    pout, plse = cea.partitioned_attention(qd, qpd, parts, return_lse=True)
+    torch.cuda.synchronize()
+    assert_attention_close(pout, plse, ro, rl, torch.bfloat16, "four partitions of 300 k keys")
