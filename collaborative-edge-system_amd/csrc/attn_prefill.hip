@@ -30,6 +30,8 @@
 //     are entirely visible or entirely hidden.
 #include <string.h>
 
+#include <algorithm>
+
 #include "cea_kernels.hpp"
 #include "cea_lds_dma.hpp"
 
@@ -147,10 +149,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
 
   // ---- XCD-aware work mapping: consecutive logical blocks share (b, kv head) and land on
   // the same XCD (blocks are dispatched round-robin over 8 XCDs).
+  // A key-split launch repeats the grid once per split, split slowest, so the workgroups of
+  // one split and KV head (which read the same tiles) stay together as well.
   const int nqb = (p.Sq + BM - 1) / BM;
   const int total = nqb * p.Hq * p.B;
+  const int nsplit = MULTI ? 1 : max(p.splits, 1);
+  const int all = total * nsplit;
   int blk = blockIdx.x;
-  if ((total & 7) == 0) blk = (blk & 7) * (total >> 3) + (blk >> 3);
+  if ((all & 7) == 0) blk = (blk & 7) * (all >> 3) + (blk >> 3);
+  const int split = MULTI ? 0 : blk / total;
+  blk -= split * total;
   const int qb = nqb - 1 - (blk % nqb);  // later (heavier causal) query blocks first
   const int bh = blk / nqb;
   const int h = bh % p.Hq;
@@ -399,9 +407,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   // ---- passes over the key block: list the tiles this workgroup needs, then stream them.
   // Under the causal rule a workgroup whose rows all have position < 0 (padding) sees no key
   // (a visible key needs 0 <= k_pos <= q_pos), so it goes straight to the epilogue.
-  const int npasses_end = p.causal && qmax_wg < 0 ? 0 : p.ntiles;
-  for (int base = 0; base < npasses_end; base += LIST_CAP) {
-    const int span = min(LIST_CAP, p.ntiles - base);
+  // tiles [t_first, t_last) of the block, all of them unless the launch splits the keys
+  const int per_split = (p.ntiles + nsplit - 1) / nsplit;
+  const int t_first = min(p.ntiles, split * per_split);
+  const int t_last = min(p.ntiles, t_first + per_split);
+  const int passes_end = p.causal && qmax_wg < 0 ? t_first : t_last;
+  for (int base = t_first; base < passes_end; base += LIST_CAP) {
+    const int span = min(LIST_CAP, t_last - base);
     int n = 0;
     for (int r0 = 0; r0 < span; r0 += NTHREADS) {
       const int t = base + r0 + tid;
@@ -477,7 +489,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   const bool empty = !(l_tot > 0.f);
   const float inv = empty ? 0.f : 1.f / l_tot;
   const float lse_new = empty ? -__builtin_inff() : m_run * fabsf(scale) + logf(l_tot);
-  float* lse_ptr = p.lse ? (float*)p.lse + b * p.ls_b + h * p.ls_h + (int64_t)row * p.ls_s
+  // a key split's partial pair (offsets 0 without splits)
+  const int64_t o_split = (int64_t)split * p.split_out;
+  float* lse_ptr = p.lse ? (float*)p.lse + (int64_t)split * p.split_lse + b * p.ls_b + h * p.ls_h +
+                               (int64_t)row * p.ls_s
                          : nullptr;
   if (p.accumulate) {
     const float lse_old = *lse_ptr;
@@ -522,7 +537,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
     if (g == 0) *lse_ptr = lse;
   } else {
     if (p.out_dtype == CEA_F32) {
-      float* orow = (float*)p.out + b * p.os_b + (int64_t)row * p.os_s + h * p.os_h;
+      float* orow = (float*)p.out + o_split + b * p.os_b + (int64_t)row * p.os_s + h * p.os_h;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -531,7 +546,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
               make_float4(oacc[dt][i4 * 4 + 0] * inv, oacc[dt][i4 * 4 + 1] * inv,
                           oacc[dt][i4 * 4 + 2] * inv, oacc[dt][i4 * 4 + 3] * inv);
     } else {
-      T* orow = (T*)p.out + b * p.os_b + (int64_t)row * p.os_s + h * p.os_h;
+      T* orow = (T*)p.out + o_split + b * p.os_b + (int64_t)row * p.os_s + h * p.os_h;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -551,7 +566,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
 template <typename T, int D, bool MULTI>
 int launch_typed(const AttnParams& p, const KvSegs& segs, hipStream_t st) {
   const int nqb = (p.Sq + BM - 1) / BM;
-  const int64_t total = (int64_t)nqb * p.Hq * p.B;
+  const int64_t total = (int64_t)nqb * p.Hq * p.B * (MULTI ? 1 : std::max(p.splits, 1));
   if (total == 0) return CEA_OK;
   CEA_REQUIRE(total < (int64_t)1 << 31, CEA_EUNSUPPORTED, "attention: grid too large");
   const hipError_t e = reserve_lds<attn_prefill_kernel<T, D, MULTI>>(Layout<D>::LDS_BYTES);
@@ -623,6 +638,18 @@ static bool prefill_block_ok(const AttnParams& p, const KvSeg& g) {
   // tiles are addressed from 64-bit bases with 32-bit offsets inside one tile, so a block may
   // span any number of bytes; list entries hold a tile of the block in 24 bits
   return ((int64_t)g.Sk + kTileKeys - 1) / kTileKeys < ((int64_t)1 << 24);
+}
+
+int prefill_key_splits(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk) {
+  // One 8-wave workgroup per compute unit at a time: below 256 workgroups part of the device
+  // idles for the whole launch (a 128-token prefill chunk at batch 1 and 32 heads has 32).
+  // Splits bring the grid to about 512 workgroups, each with at least 8 tiles of keys; their
+  // partials are merged afterwards.
+  const int64_t grid = (Sq + BM - 1) / BM * Hq * B;
+  const int64_t tiles = (Sk + kTileKeys - 1) / kTileKeys;
+  if (grid <= 0 || grid >= 256) return 1;
+  int64_t s = std::min<int64_t>({(int64_t)kMaxKeySplits, (512 + grid - 1) / grid, tiles / 8});
+  return s >= 2 ? (int)s : 1;
 }
 
 bool prefill_mfma_supported(const AttnParams& p) {

@@ -79,6 +79,13 @@ static size_t tile_bytes(int64_t B, int64_t Sk) {
   return align_up((size_t)(B * ntiles_of(Sk)) * sizeof(TileInfo), 256);
 }
 
+// Workspace of a key-split prefill call after its tile summaries: one f32 (out, lse) pair per
+// split, [B, Sq, Hq, D] and [B, Hq, Sq] each.
+static size_t split_bytes(int S, int64_t B, int64_t Sq, int64_t Hq, int64_t D) {
+  if (S <= 1) return 0;
+  return (size_t)S * ((size_t)B * Sq * Hq * D + (size_t)B * Hq * Sq) * sizeof(float);
+}
+
 // Builds the attention parameter block for one KV block; validates shapes and dtypes.
 static int make_attn_params(AttnParams* p, const cea_tensor* q, const cea_tensor* k,
                             const cea_tensor* v, const cea_tensor* q_pos,
@@ -271,6 +278,48 @@ static bool use_decode(const AttnParams& p) {
 // Runs one attention call with a prepared parameter block.  allow_decode = false keeps the
 // call off the split-KV decode kernels, whose workspace (chunk partials) is larger than the
 // tile summaries the other kernels need.
+// A prefill call whose query blocks alone give too few workgroups to fill the device (short
+// query blocks against long key blocks: prefill chunks, decode shapes the split-KV kernels do
+// not take): the block's tiles are dealt to S groups of workgroups, each writing a partial
+// (out, lse) into the workspace, and the partials are merged with merge_attention_list's
+// formula into the caller's out (f32 or the query dtype) and lse.
+static int run_prefill_split(const AttnParams& p, int S, char* ws, hipStream_t st) {
+  const int64_t n_out = (int64_t)p.B * p.Sq * p.Hq * p.D, n_lse = (int64_t)p.B * p.Hq * p.Sq;
+  float* po = (float*)ws;
+  float* pl = po + S * n_out;
+  AttnParams sp = p;
+  sp.splits = S;
+  sp.split_out = n_out;
+  sp.split_lse = n_lse;
+  sp.out = po;
+  sp.lse = pl;
+  sp.out_dtype = CEA_F32;
+  sp.os_b = (int64_t)p.Sq * p.Hq * p.D; sp.os_s = (int64_t)p.Hq * p.D; sp.os_h = p.D;
+  sp.ls_b = (int64_t)p.Hq * p.Sq; sp.ls_h = p.Sq; sp.ls_s = 1;
+  int rc = launch_attn_prefill_mfma(sp, st);
+  if (rc) return rc;
+  MergeParams m;
+  memset(&m, 0, sizeof(m));
+  m.n = S;
+  m.pairwise = 0;
+  m.B = p.B; m.Sq = p.Sq; m.H = p.Hq; m.D = p.D;
+  m.dtype = CEA_F32;
+  m.out_dtype = p.out_dtype;
+  for (int i = 0; i < S; ++i) {
+    m.outs[i] = po + i * n_out;
+    m.lses[i] = pl + i * n_lse;
+    m.os[i][0] = sp.os_b; m.os[i][1] = sp.os_s; m.os[i][2] = sp.os_h;
+    m.ls[i][0] = sp.ls_b; m.ls[i][1] = sp.ls_h; m.ls[i][2] = sp.ls_s;
+  }
+  m.out = p.out;
+  m.dos[0] = p.os_b; m.dos[1] = p.os_s; m.dos[2] = p.os_h;
+  if (p.lse) {
+    m.lse = p.lse;
+    m.dls[0] = p.ls_b; m.dls[1] = p.ls_h; m.dls[2] = p.ls_s;
+  }
+  return launch_merge(m, st);
+}
+
 static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t st,
                          bool allow_decode = true) {
   if (allow_decode && p.Sk > 0 && use_decode(p))
@@ -283,6 +332,13 @@ static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t s
     p.tiles = (const TileInfo*)ws;
     int rc = launch_tile_info(p.k_pos, p.kps_b, p.kps_s, p.B, p.Sk, (TileInfo*)ws, p.ntiles, st);
     if (rc) return rc;
+    // key splits when they help and the workspace holds their partials (a smaller workspace,
+    // such as the slice a partitioned call leaves, runs the unsplit launch)
+    if (!p.accumulate && !p.final_out) {
+      const int S = prefill_key_splits(p.B, p.Sq, p.Hq, p.Sk);
+      if (S > 1 && ws_bytes >= need + split_bytes(S, p.B, p.Sq, p.Hq, p.D))
+        return run_prefill_split(p, S, ws + need, st);
+    }
     return launch_attn_prefill_mfma(p, st);
   }
   return launch_attn_generic(p, st);
@@ -337,12 +393,22 @@ const char* cea_last_error(void) { return cea::last_error(); }
 
 int cea_version(void) { return 100; }
 
-size_t cea_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int64_t Hkv,
-                                     int64_t D, int32_t in_dtype) {
+// with_splits: room for the partials of a key-split prefill launch as well (the no-allocation
+// entry point refuses only calls whose other scratch does not fit, and runs key splits when
+// their partials fit too)
+static size_t attention_ws_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int64_t Hkv,
+                                 int64_t D, int32_t in_dtype, bool with_splits) {
   if (B <= 0 || Sk <= 0) return 256;
   size_t need = tile_bytes(B, Sk);
+  if (with_splits && (in_dtype == CEA_BF16 || in_dtype == CEA_F16) && (D == 64 || D == 128))
+    need += split_bytes(prefill_key_splits(B, Sq, Hq, Sk), B, Sq, Hq, D);
   const size_t dec = decode_ws_bytes(&Sk, 1, B, Sq, Hq, Hkv, D, in_dtype);
   return dec > need ? dec : need;
+}
+
+size_t cea_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int64_t Hkv,
+                                     int64_t D, int32_t in_dtype) {
+  return attention_ws_bytes(B, Sq, Hq, Sk, Hkv, D, in_dtype, true);
 }
 
 int cea_attention_with_lse(const cea_tensor* q, const cea_tensor* k, const cea_tensor* v,
@@ -366,8 +432,7 @@ int cea_attention_with_lse_noalloc(const cea_tensor* q, const cea_tensor* k, con
   int rc = make_attn_params(&p, q, k, v, q_pos, k_pos, causal, scale, kv_map, kv_map_len, out,
                             lse, accumulate);
   if (rc) return rc;
-  const size_t need = cea_attention_workspace_bytes(p.B, p.Sq, p.Hq, p.Sk, p.Hkv, p.D,
-                                                    p.in_dtype);
+  const size_t need = attention_ws_bytes(p.B, p.Sq, p.Hq, p.Sk, p.Hkv, p.D, p.in_dtype, false);
   CEA_REQUIRE(need <= (size_t)CEA_NOALLOC_SCRATCH_BYTES, CEA_ENOSPACE,
               "attention_with_lse_noalloc: this call needs %zu bytes of scratch, the static "
               "scratch holds %zu (use cea_attention_with_lse with a workspace)",

@@ -35,6 +35,11 @@ struct AttnParams {
   void* final_out;
   int64_t fs_b, fs_s, fs_h;
   int32_t final_dtype;
+  // key-split prefill launches (0 or 1: none): the block's tiles are dealt in equal runs to
+  // `splits` groups of workgroups; group i writes its partial (out, lse) at
+  // out + i * split_out and lse + i * split_lse (elements)
+  int32_t splits;
+  int64_t split_out, split_lse;
 };
 
 // KV blocks of one prefill launch, in the order their tiles are visited (a ring share's
@@ -198,6 +203,10 @@ bool prefill_mfma_supported(const AttnParams& p);
 // p carries q / out / lse / head map / row strides; the blocks come from segs (p.k, p.v,
 // p.k_pos and p.Sk are not read); p.ntiles and p.tiles cover all blocks
 bool prefill_segs_supported(const AttnParams& p, const KvSegs& segs);
+// Key splits worth a prefill launch of these shapes (1: none): enough workgroups to fill the
+// device when the query blocks alone would not.  At most kMaxKeySplits (one n-way merge).
+constexpr int kMaxKeySplits = CEA_MAX_PARTS;
+int prefill_key_splits(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk);
 int launch_attn_prefill_mfma(const AttnParams& p, hipStream_t s);
 int launch_attn_prefill_segs(const AttnParams& p, const KvSegs& segs, hipStream_t s);
 bool f32_mfma_supported(const AttnParams& p);
