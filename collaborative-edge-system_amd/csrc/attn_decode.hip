@@ -204,8 +204,9 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   __shared__ float red_l[NW][NR];
 
   // 1-D grid: pair items of rows [0, pair_rows), then single-chunk items of the other rows;
-  // item fastest, then unit, then batch row - except per-head units, which go fastest so that
-  // the units reading one KV head's chunk run side by side and share its reads in the caches
+  // item fastest, then unit, then batch row - except when several units read one KV head
+  // (per_head): units go fastest then, so those reading one KV head's chunk run side by side
+  // and share its reads in the caches
   const int total_chunks = p.chunk_begin[p.nparts];
   int b, unit, item;
   {
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
       item = r % ni;
     }
   }
-  const int kvh = p.per_head ? (int)p.map.kv[unit] : unit;  // KV head the unit reads
+  const int kvh = p.map.kv_of(unit * p.G);  // KV head the unit's query heads read
   const DecodeItem it = item_of(p, b, item);
   const int part = it.part, chunk = it.chunk, nch = it.nch;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   const int s = (row / p.Hq) % p.Sq;
   const int b = row / (p.Hq * p.Sq);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int unit = p.per_head ? h : p.map.kv_of(h);  // the work unit that computed this head
+  const int unit = h / p.G;  // the work unit that computed this head
   const int r = s * p.G + (h - unit * p.G);
   const int total_chunks = p.chunk_begin[p.nparts];
   const int total = items_of_row(p, b);  // work items (partials) of this batch row
@@ -708,9 +709,10 @@ bool decode_supported(int32_t Sq, int32_t Hq, int32_t Hkv, int32_t D, int32_t dt
                       const HeadMap& map) {
   if (!(dtype == CEA_BF16 || dtype == CEA_F16)) return false;
   if (!(D == 64 || D == 128)) return false;
-  // the regular grouping shares each K/V row among the G query heads of a KV head; any other
-  // map runs one unit per query head
-  if (map.group > 0) return decode_rows(Sq, Hq / Hkv) != 0;
+  // the regular grouping shares each K/V row among the query heads of a KV head (all of
+  // them, or a divisor of the group whose rows fit one unit); any other map runs one unit per
+  // query head
+  if (map.group > 0) return decode_rows(Sq, 1) != 0;
   return Hq <= CEA_MAX_MAPPED_HEADS && decode_rows(Sq, 1) != 0;
 }
 

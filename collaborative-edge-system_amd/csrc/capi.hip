@@ -160,13 +160,23 @@ struct DecodePlan {
   size_t vis_offset, mask_offset;
 };
 
-// Work units of the decode kernels for a head map: the KV heads (G = Hq / Hkv query heads
-// each) for the regular grouping, the query heads (G = 1) for any other map.
+// Work units of the decode kernels: G consecutive query heads that read one KV head, whose
+// Sq * G rows share every K/V tile.  The regular grouping takes a KV head's whole group
+// (G = Hq / Hkv) when its rows fit one unit, else the largest divisor of the group whose rows
+// do (two units of 16 heads for 32 heads on one KV head); any other map takes one query head
+// per unit (G = 1).  Units that split a KV head's group, and query-head units, go fastest in
+// the grid (per_head), so the units reading one KV head's tiles run side by side.
 struct DecodeUnits {
   int32_t units, G, per_head;
 };
-static DecodeUnits decode_units(int64_t Hq, int64_t Hkv, const HeadMap& map) {
-  if (map.group > 0) return {(int32_t)Hkv, (int32_t)(Hq / Hkv), 0};
+static DecodeUnits decode_units(int64_t Hq, int64_t Hkv, int64_t Sq, const HeadMap& map) {
+  if (map.group > 0) {
+    const int64_t G = Hq / Hkv;
+    if (decode_rows((int32_t)Sq, (int32_t)G) != 0) return {(int32_t)Hkv, (int32_t)G, 0};
+    for (int64_t gs = G - 1; gs > 1; --gs)
+      if (G % gs == 0 && decode_rows((int32_t)Sq, (int32_t)gs) != 0)
+        return {(int32_t)(Hq / gs), (int32_t)gs, 1};
+  }
   return {(int32_t)Hq, 1, 1};
 }
 
@@ -195,8 +205,10 @@ static size_t decode_ws_bytes(const int64_t* Sk, int n, int64_t B, int64_t Sq, i
   regular.group = 1;
   size_t need = 0;
   if (Hkv > 0 && Hq % Hkv == 0 &&
-      decode_supported((int32_t)Sq, (int32_t)Hq, (int32_t)Hkv, (int32_t)D, dtype, regular))
-    need = plan_decode(Sk, n, B, Sq, Hkv, Hq / Hkv, D).partial_bytes;
+      decode_supported((int32_t)Sq, (int32_t)Hq, (int32_t)Hkv, (int32_t)D, dtype, regular)) {
+    const DecodeUnits du = decode_units(Hq, Hkv, Sq, regular);
+    need = plan_decode(Sk, n, B, Sq, du.units, du.G, D).partial_bytes;
+  }
   HeadMap table;
   table.group = 0;
   if (Hkv > 0 && decode_supported((int32_t)Sq, (int32_t)Hq, (int32_t)Hkv, (int32_t)D, dtype, table)) {
@@ -212,7 +224,7 @@ static int run_decode(const AttnParams* blocks, int n, cea_tensor* part_out, cea
   const AttnParams& a = blocks[0];
   int64_t sks[CEA_MAX_PARTS];
   for (int i = 0; i < n; ++i) sks[i] = blocks[i].Sk;
-  const DecodeUnits du = decode_units(a.Hq, a.Hkv, a.map);
+  const DecodeUnits du = decode_units(a.Hq, a.Hkv, a.Sq, a.map);
   const DecodePlan pl = plan_decode(sks, n, a.B, a.Sq, du.units, du.G, a.D);
   CEA_REQUIRE(ws != nullptr && ws_bytes >= pl.partial_bytes, CEA_ENOSPACE,
               "decode: workspace of %zu bytes needed, %zu given", pl.partial_bytes, ws_bytes);
@@ -263,7 +275,7 @@ static int run_decode(const AttnParams* blocks, int n, cea_tensor* part_out, cea
 static bool use_decode(const AttnParams& p) {
   if (!decode_supported(p.Sq, p.Hq, p.Hkv, p.D, p.in_dtype, p.map)) return false;
   const int64_t sk = p.Sk;
-  const DecodeUnits du = decode_units(p.Hq, p.Hkv, p.map);
+  const DecodeUnits du = decode_units(p.Hq, p.Hkv, p.Sq, p.map);
   if (plan_decode(&sk, 1, p.B, p.Sq, du.units, du.G, p.D).total_chunks > kDecodeMaxChunks) return false;
   if (!(p.out_dtype == CEA_F32 || p.out_dtype == p.in_dtype)) return false;
   if (p.accumulate && p.out_dtype != CEA_F32) return false;
@@ -952,7 +964,7 @@ int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* 
       dec = dec && use_decode(blocks[i]);
     }
     if (dec) {
-      const DecodeUnits du = decode_units(Hq, blocks[0].Hkv, blocks[0].map);
+      const DecodeUnits du = decode_units(Hq, blocks[0].Hkv, Sq, blocks[0].map);
       dec = plan_decode(sks, n, B, Sq, du.units, du.G, D).total_chunks <= kDecodeMaxChunks;
     }
     if (dec && part_out) {

@@ -102,18 +102,18 @@ struct DecodeParams {
   int32_t causal;
   int32_t in_dtype;
   HeadMap map;
-  // partial results [B, Hkv, total_chunks, NR rows (s, g)] x {D + 2} floats (o unnormalised,
+  // partial results [B, units, total_chunks, NR rows (s, g)] x {D + 2} floats (o unnormalised,
   // m, l); per-key visibility words [B, total_chunks, chunk] (bit s: query s sees the key);
   // per-chunk masks [B, total_chunks] of 16-key tiles with a visible key
   float* partial;
   uint16_t* vis;
   uint64_t* tile_mask;
-  int32_t G;                 // query heads per KV head handled by one work item
-  // work units per batch row: the KV heads (G query heads each, kv = h / G), or, for an
-  // explicit head map that is not that grouping (per_head = 1), the query heads themselves
-  // (G = 1; unit h reads KV head map.kv[h])
+  int32_t G;                 // query heads of one work unit (all read one KV head)
+  // work units per batch row: unit u holds query heads u*G .. u*G+G-1 and reads KV head
+  // map.kv_of(u*G) - a KV head's whole group, part of it, or (G = 1) one query head of an
+  // explicit map
   int32_t units;
-  int32_t per_head;
+  int32_t per_head;          // 1: units fastest in the grid (several units per KV head)
   // outputs of the reduction
   void* part_out[CEA_MAX_PARTS];   // optional per-partition (out, lse), f32
   void* part_lse[CEA_MAX_PARTS];

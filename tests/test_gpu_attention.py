@@ -348,3 +348,27 @@ def test_decode_against_more_than_a_million_keys(cea, dev):
     pout, plse = cea.partitioned_attention(qd, qpd, parts, return_lse=True)
     torch.cuda.synchronize()
     assert_attention_close(pout, plse, ro, rl, torch.bfloat16, "four partitions of 300 k keys")
+
+
+@pytest.mark.parametrize("shape", [(3, 1, 5000, 32, 1, 128), (2, 2, 3000, 16, 1, 64),
+                                   (2, 3, 4000, 24, 4, 128)],
+                         ids=["mqa-g32", "g16-two-tokens", "g6-three-tokens"])
+def test_decode_with_more_rows_per_kv_head_than_a_unit(cea, dev, shape):
+    """Decode shapes whose query rows per KV head (Sq x G) exceed the 16 a split-KV unit
+    takes run one unit per query head, each reading its KV head's tiles: against the oracle,
+    with a -1-tailed cache per sequence."""
+    B, Sq, Sk, Hq, Hkv, D = shape
+    g = torch.Generator().manual_seed(Sk)
+    q = torch.randn(B, Sq, Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Sk, Hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Sk, Hkv, D, generator=g).to(torch.bfloat16)
+    lens = torch.randint(Sq, Sk + 1, (B,), generator=g)
+    slots = torch.arange(Sk).view(1, Sk)
+    kp = torch.where(slots < lens.view(-1, 1), slots, torch.full_like(slots, -1))
+    qp = lens.view(-1, 1) - Sq + torch.arange(Sq).view(1, Sq)
+    ro, rl = ref.attention_with_lse(q, k, v, qp, kp)
+    out, lse = cea.attention_with_lse(q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev))
+    plain = cea.attention.attention(q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev))
+    torch.cuda.synchronize()
+    assert_attention_close(out, lse, ro, rl, torch.bfloat16, str(shape))
+    assert (plain.cpu().double() - ro.double()).abs().max().item() <= 2e-2

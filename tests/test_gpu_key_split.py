@@ -1,7 +1,7 @@
 """Key-split prefill launches, through the C ABI and the operator library.
 
 Short query blocks against long key blocks (a prefill chunk against the cache before it, or a
-decode shape whose rows per KV head exceed what the split-KV decode kernels take) give too few
+few tokens with more query rows than the split-KV decode kernels take) give too few
 query blocks to fill the device; the prefill route then deals the key tiles to several groups
 of workgroups and merges their partial (out, lse) pairs.  Each case is checked against the
 oracle at the bf16 tolerances, against the unsplit launch (the same call given only the
@@ -23,7 +23,7 @@ CASES = [
     # B, Sq, Sk, Hq, Hkv, D, positions, causal
     (1, 128, 20000, 32, 8, 128, "chunk", True),   # a 128-token prefill chunk at batch 1
     (2, 40, 3000, 8, 1, 64, "chunk", True),       # 8 query heads per KV head: 320 rows
-    (1, 1, 9000, 32, 1, 128, "chunk", True),      # one token, 32 query heads on one KV head
+    (1, 20, 9000, 8, 8, 128, "chunk", True),      # 20 tokens, one query head per KV head
     (1, 100, 7000, 16, 4, 128, "padded", True),   # padded keys and padded query rows
     (1, 64, 5000, 8, 2, 64, "chunk", False),      # no causal rule
 ]
