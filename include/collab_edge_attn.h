@@ -69,7 +69,9 @@ int cea_version(void);
 /*
  * Bytes of device workspace cea_attention_with_lse needs for these shapes (q: [B,Sq,Hq,D],
  * k: [B,Sk,Hkv,D]).  The workspace holds per-key-tile position summaries and, for short
- * query blocks, split-KV partial results.
+ * query blocks, split-KV partial results; for query blocks too few to fill the device
+ * against long key blocks, the partial (out, lse) pairs of a key-split launch.  A smaller
+ * workspace that still holds the summaries runs such a call without key splits.
  */
 size_t cea_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int64_t Hkv,
                                      int64_t D, int32_t in_dtype);
