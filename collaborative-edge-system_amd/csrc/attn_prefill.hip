@@ -150,9 +150,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   // ---- XCD-aware work mapping: consecutive logical blocks share (b, kv head) and land on
   // the same XCD (blocks are dispatched round-robin over 8 XCDs).
   // A key-split launch repeats the grid once per split, split slowest, so the workgroups of
-  // one split and KV head (which read the same tiles) stay together as well.
-  const int nqb = (p.Sq + BM - 1) / BM;
-  const int total = nqb * p.Hq * p.B;
+  // one split and KV head (which read the same tiles) stay together as well.  A workgroup
+  // holds hp query heads of one KV head's group (NWAVES / hp waves and BM / hp rows each), so
+  // short query blocks do not leave most of its rows empty.
+  const int hp = MULTI ? 1 : max(p.heads_per_wg, 1);
+  const int rows_pb = BM / hp;  // query rows of one head in a workgroup
+  const int nqb = (p.Sq + rows_pb - 1) / rows_pb;
+  const int ngroups = p.Hq / hp;
+  const int total = nqb * ngroups * p.B;
   const int nsplit = MULTI ? 1 : max(p.splits, 1);
   const int all = total * nsplit;
   int blk = blockIdx.x;
@@ -161,18 +166,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   blk -= split * total;
   const int qb = nqb - 1 - (blk % nqb);  // later (heavier causal) query blocks first
   const int bh = blk / nqb;
-  const int h = bh % p.Hq;
-  const int b = bh / p.Hq;
-  const int kvh = p.map.kv_of(h);
+  const int hg = bh % ngroups;
+  const int b = bh / ngroups;
+  const int waves_ph = NWAVES / hp;
+  const int h = hg * hp + wave / waves_ph;   // this wave's query head
+  const int kvh = p.map.kv_of(hg * hp);      // one KV head for the whole workgroup
+  const int qrow0 = qb * rows_pb + (wave % waves_ph) * 32;  // this wave's first query row
 
-  const int row = qb * BM + wave * 32 + r;
+  const int row = qrow0 + r;
   const bool row_ok = row < p.Sq;
   const int64_t qpos = row_ok ? p.q_pos[b * p.qps_b + (int64_t)row * p.qps_s] : 0;
 
   // ---- query position ranges of the wave and of the workgroup
   const int64_t qmin_w = wave_min_i64(row_ok ? qpos : INT64_MAX);
   const int64_t qmax_w = wave_max_i64(row_ok ? qpos : INT64_MIN);
-  const bool wave_active = __builtin_amdgcn_readfirstlane(qb * BM + wave * 32 < p.Sq ? 1 : 0);
+  const bool wave_active = __builtin_amdgcn_readfirstlane(qrow0 < p.Sq ? 1 : 0);
   if (lane == 0) {
     red_q[wave] = qmax_w;
     red_qmin[wave] = qmin_w;
@@ -565,8 +573,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
 
 template <typename T, int D, bool MULTI>
 int launch_typed(const AttnParams& p, const KvSegs& segs, hipStream_t st) {
-  const int nqb = (p.Sq + BM - 1) / BM;
-  const int64_t total = (int64_t)nqb * p.Hq * p.B * (MULTI ? 1 : std::max(p.splits, 1));
+  const int hp = MULTI ? 1 : std::max(p.heads_per_wg, 1);
+  const int nqb = (p.Sq + BM / hp - 1) / (BM / hp);
+  const int64_t total = (int64_t)nqb * (p.Hq / hp) * p.B * (MULTI ? 1 : std::max(p.splits, 1));
   if (total == 0) return CEA_OK;
   CEA_REQUIRE(total < (int64_t)1 << 31, CEA_EUNSUPPORTED, "attention: grid too large");
   const hipError_t e = reserve_lds<attn_prefill_kernel<T, D, MULTI>>(Layout<D>::LDS_BYTES);
@@ -640,12 +649,27 @@ static bool prefill_block_ok(const AttnParams& p, const KvSeg& g) {
   return ((int64_t)g.Sk + kTileKeys - 1) / kTileKeys < ((int64_t)1 << 24);
 }
 
-int prefill_key_splits(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk) {
+int prefill_heads_per_wg(int64_t Sq, int64_t G) {
+  // fewest padded query rows per head (ceil(Sq / rows) * rows - Sq with BM / hp rows of a
+  // head per workgroup); the smallest count on ties, so query blocks that are multiples of
+  // BM keep one head per workgroup
+  int best = 1;
+  int64_t best_pad = (Sq + BM - 1) / BM * BM - Sq;
+  for (int hp = 2; hp <= NWAVES && G > 0 && G % hp == 0; hp *= 2) {
+    const int64_t rows = BM / hp;
+    const int64_t pad = (Sq + rows - 1) / rows * rows - Sq;
+    if (pad < best_pad) best = hp, best_pad = pad;
+  }
+  return best;
+}
+
+int prefill_key_splits(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int hp) {
   // One 8-wave workgroup per compute unit at a time: below 256 workgroups part of the device
   // idles for the whole launch (a 128-token prefill chunk at batch 1 and 32 heads has 32).
   // Splits bring the grid to about 512 workgroups, each with at least 8 tiles of keys; their
   // partials are merged afterwards.
-  const int64_t grid = (Sq + BM - 1) / BM * Hq * B;
+  const int64_t rows = BM / hp;
+  const int64_t grid = (Sq + rows - 1) / rows * (Hq / hp) * B;
   const int64_t tiles = (Sk + kTileKeys - 1) / kTileKeys;
   if (grid <= 0 || grid >= 256) return 1;
   int64_t s = std::min<int64_t>({(int64_t)kMaxKeySplits, (512 + grid - 1) / grid, tiles / 8});

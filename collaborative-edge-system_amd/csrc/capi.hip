@@ -344,10 +344,11 @@ static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t s
     p.tiles = (const TileInfo*)ws;
     int rc = launch_tile_info(p.k_pos, p.kps_b, p.kps_s, p.B, p.Sk, (TileInfo*)ws, p.ntiles, st);
     if (rc) return rc;
+    p.heads_per_wg = prefill_heads_per_wg(p.Sq, p.map.group > 0 ? p.map.group : 0);
     // key splits when they help and the workspace holds their partials (a smaller workspace,
     // such as the slice a partitioned call leaves, runs the unsplit launch)
     if (!p.accumulate && !p.final_out) {
-      const int S = prefill_key_splits(p.B, p.Sq, p.Hq, p.Sk);
+      const int S = prefill_key_splits(p.B, p.Sq, p.Hq, p.Sk, p.heads_per_wg);
       if (S > 1 && ws_bytes >= need + split_bytes(S, p.B, p.Sq, p.Hq, p.D))
         return run_prefill_split(p, S, ws + need, st);
     }
@@ -412,8 +413,12 @@ static size_t attention_ws_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, 
                                  int64_t D, int32_t in_dtype, bool with_splits) {
   if (B <= 0 || Sk <= 0) return 256;
   size_t need = tile_bytes(B, Sk);
-  if (with_splits && (in_dtype == CEA_BF16 || in_dtype == CEA_F16) && (D == 64 || D == 128))
-    need += split_bytes(prefill_key_splits(B, Sq, Hq, Sk), B, Sq, Hq, D);
+  // (the regular grouping's plan: an explicit map has one head per workgroup, so more
+  // workgroups and no more splits)
+  if (with_splits && (in_dtype == CEA_BF16 || in_dtype == CEA_F16) && (D == 64 || D == 128)) {
+    const int hp = prefill_heads_per_wg(Sq, Hkv > 0 && Hq % Hkv == 0 ? Hq / Hkv : 0);
+    need += split_bytes(prefill_key_splits(B, Sq, Hq, Sk, hp), B, Sq, Hq, D);
+  }
   const size_t dec = decode_ws_bytes(&Sk, 1, B, Sq, Hq, Hkv, D, in_dtype);
   return dec > need ? dec : need;
 }

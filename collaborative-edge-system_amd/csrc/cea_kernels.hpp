@@ -40,6 +40,9 @@ struct AttnParams {
   // out + i * split_out and lse + i * split_lse (elements)
   int32_t splits;
   int64_t split_out, split_lse;
+  // prefill workgroups hold this many query heads of one KV head's group (0 or 1: one), each
+  // with 1 / heads_per_wg of the workgroup's query rows
+  int32_t heads_per_wg;
 };
 
 // KV blocks of one prefill launch, in the order their tiles are visited (a ring share's
@@ -206,7 +209,10 @@ bool prefill_segs_supported(const AttnParams& p, const KvSegs& segs);
 // Key splits worth a prefill launch of these shapes (1: none): enough workgroups to fill the
 // device when the query blocks alone would not.  At most kMaxKeySplits (one n-way merge).
 constexpr int kMaxKeySplits = CEA_MAX_PARTS;
-int prefill_key_splits(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk);
+int prefill_key_splits(int64_t B, int64_t Sq, int64_t Hq, int64_t Sk, int heads_per_wg);
+// Query heads per prefill workgroup for Sq query rows and G query heads per KV head (G = 0:
+// an explicit head map, one head per workgroup): 1, 2, 4 or 8.
+int prefill_heads_per_wg(int64_t Sq, int64_t G);
 int launch_attn_prefill_mfma(const AttnParams& p, hipStream_t s);
 int launch_attn_prefill_segs(const AttnParams& p, const KvSegs& segs, hipStream_t s);
 bool f32_mfma_supported(const AttnParams& p);
