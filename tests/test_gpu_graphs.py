@@ -1,8 +1,9 @@
 """HIP-graph capture of the operators.
 
-* Replays of captured ring-share, distributed-KV decode and layer-op calls equal the eager
-  results on every replay, with eager work on the device between the replays (the kernels
-  write every scratch value they read in the same call and record no memset).
+* Replays of captured ring-share, distributed-KV decode, key-split prefill and layer-op calls
+  equal the eager results on every replay, with eager work on the device between the
+  replays (the kernels write every scratch value they read in the same call and record no
+  memset).
 * The operator library's per-stream workspace: a buffer that a capture recorded stays
   allocated when a later, larger call on that stream replaces it, so replays never write into
   memory the allocator has handed out again.
@@ -115,3 +116,25 @@ def test_layer_ops_replays(cea, dev):
         return y, h
 
     _replays_match(step, lambda: cea.gated_mul(up, gate, "gelu"))
+
+
+def test_key_split_and_subgroup_decode_replays(cea, dev):
+    """A prefill chunk that takes the key-split route (partials in the workspace, then the
+    list merge) and a decode step with 32 query heads on one KV head (sub-group units)."""
+    q, k, v, pos = _attn_inputs(dev, 6000, 7, hq=8, hkv=2)
+    qc, qpc = q[:, -96:], pos[:, -96:]
+    g = torch.Generator().manual_seed(8)
+    dq = torch.randn(2, 1, 32, 128, generator=g).to(torch.bfloat16).to(dev)
+    dk = torch.randn(2, 3000, 1, 128, generator=g).to(torch.bfloat16).to(dev)
+    dv = torch.randn(2, 3000, 1, 128, generator=g).to(torch.bfloat16).to(dev)
+    dkp = torch.arange(3000).repeat(2, 1).to(dev)
+    dqp = torch.full((2, 1), 2999).to(dev)
+
+    def step():
+        out, lse = cea.attention_with_lse(qc, k, v, qpc, pos)
+        plain = cea.attention.attention(qc, k, v, qpc, pos)
+        dout, dlse = cea.attention_with_lse(dq, dk, dv, dqp, dkp)
+        return out, lse, plain, dout, dlse
+
+    bq, bk, bv, bpos = _attn_inputs(dev, 2048, 9)
+    _replays_match(step, lambda: cea.attention_with_lse(bq, bk, bv, bpos, bpos))
