@@ -102,6 +102,20 @@ def _event_timed(fn, steps: int, warmup: int, torch, dev):
     return (time.perf_counter() - t0) / steps, a.elapsed_time(b) / steps
 
 
+def _event_timed_rounds(fn, steps: int, warmup: int, torch, dev, rounds: int = 5,
+                        warm_ms: float = 100.0):
+    """For steps of a fraction of a millisecond: warm up for at least ``warm_ms`` of GPU work
+    (the clocks settle; a single round right after a few warm-up steps reads several percent
+    slow), then ``rounds`` rounds of ``steps`` timed with HIP events.  Returns (wall seconds
+    per call of the median round, GPU milliseconds per call of the median round)."""
+    _, first_ms = _event_timed(fn, max(1, steps), warmup, torch, dev)
+    extra = int(warm_ms / max(first_ms, 1e-3))
+    for _ in range(min(extra, 5000)):
+        fn()
+    res = sorted((_event_timed(fn, steps, 0, torch, dev) for _ in range(rounds)), key=lambda r: r[1])
+    return res[len(res) // 2]
+
+
 def bench_ring(cea, torch, steps, warmup, dev):
     """The headline: ``ring_attention`` over the four KV blocks of the ring share, one
     ``cea_ring_attention`` call (one tile-summary launch over the four blocks + one prefill
@@ -161,8 +175,9 @@ def bench_decode(cea, torch, steps, warmup, dev, hq=32, hkv=8, d=128):
         return cea.distributed_kv_attention(w.q, k0, v0, w.q_pos, p0, comm)
 
     # GPU time of the timed steps (HIP events on the launch stream): the step is three short
-    # kernels, so the wall clock of 20 steps also holds the host's first-launch latency
-    sec, gpu_ms = _event_timed(step, steps, warmup, torch, dev)
+    # kernels, so the wall clock of 20 steps also holds the host's first-launch latency; the
+    # median of 5 rounds after a 100 ms warm-up (steady clocks)
+    sec, gpu_ms = _event_timed_rounds(step, steps, warmup, torch, dev)
     gbs = w.bytes / (gpu_ms * 1e-3) / 1e9
     return {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
             "ms_per_step": round(gpu_ms, 4), "wall_ms_per_step": round(sec * 1e3, 4),
@@ -288,6 +303,23 @@ def bench_ulysses(cea, torch, steps, warmup, dev):
             "flop": w.flop, "valid_tokens": w.valid,
             "workload": "Ulysses sp=8 share: 65536 tokens, 8/2 heads, D=128, bf16, causal, "
                         "4 packed sequences + right padding, emits f32 lse"}
+
+
+def bench_prefill_chunk(cea, torch, steps, warmup, dev):
+    """A short query block against a long key block: the key-split route (several workgroup
+    groups per query block, partials merged) with two query heads per workgroup."""
+    w = cea.workloads.prefill_chunk(device=dev)
+
+    def step():
+        return cea.attention_with_lse(w.q, w.k, w.v, w.q_pos, w.k_pos)
+
+    sec, gpu_ms = _event_timed_rounds(step, steps, warmup, torch, dev)
+    tf = w.flop / (gpu_ms * 1e-3) / 1e12
+    return {"value": round(tf, 1), "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+            "ms_per_step": round(gpu_ms, 4), "wall_ms_per_step": round(sec * 1e3, 4),
+            "flop": w.flop,
+            "workload": "prefill chunk: 128 tokens at batch 1 against 32768 keys, 32/8 heads, "
+                        "D=128, bf16, causal, emits f32 lse"}
 
 
 def bench_f32_split(cea, torch, steps, warmup, dev):
@@ -527,7 +559,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of: ring,decode,layers,kvappend,ulysses,wire,f32,proj")
+                    help="comma list of: ring,decode,layers,kvappend,ulysses,chunk,wire,f32,proj")
     ap.add_argument("--trace-summary", default="", metavar="CSV",
                     help="only summarise a rocprofv3 kernel-trace CSV (the last --last "
                          "dispatches of every kernel) and exit")
@@ -579,6 +611,9 @@ def main() -> int:
     if want("ulysses"):
         _log("ulysses share")
         secondary["ulysses_share"] = bench_ulysses(cea, torch, max(5, args.steps // 2), args.warmup, dev)
+    if want("chunk"):
+        _log("prefill chunk against a long key block")
+        secondary["prefill_chunk"] = bench_prefill_chunk(cea, torch, args.steps, args.warmup, dev)
     if want("wire"):
         _log("wire formats (Ulysses all-to-alls, packed distributed-KV merge)")
         secondary["wire"] = bench_wire(cea, torch, args.steps, args.warmup, dev)

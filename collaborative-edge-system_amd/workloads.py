@@ -21,6 +21,9 @@ CPU oracle and the GPU see bit-identical inputs.
   (8192 tokens, 4096 -> 32/8/8 heads x 128) projections of a Llama-3-8B-shaped layer, bf16.
 * ``kv_append``        - one rank's 8192-token prefill chunk (8 KV heads, D=128, bf16, theta
   1e4) rotated and appended into a head-major cache that already holds 8192 tokens.
+* ``prefill_chunk``    - one 128-token chunk of a chunked prefill (engine.py:91-92) at batch
+  1 against the 32768 keys it sees (the cache before it and itself), 32/8 heads, D=128, bf16,
+  causal: few query blocks against a long key block.
 """
 
 from __future__ import annotations
@@ -333,3 +336,30 @@ def kv_append(device="cpu", seed: int = 0, n: int = 8192, heads: int = 8, head_d
     cache_v = torch.zeros_like(cache_k)
     cache_pos = torch.full((1, cap), -1, dtype=torch.int64, device=device)
     return KVAppend(k, v, pos, cos, sin, cache_k, cache_v, cache_pos, cached)
+
+
+# --------------------------------------------------------------------------------------
+@dataclass
+class PrefillChunk:
+    q: torch.Tensor        # [B, chunk, hq, d]
+    k: torch.Tensor        # [B, keys, hkv, d]
+    v: torch.Tensor
+    q_pos: torch.Tensor    # [B, chunk]: the last chunk positions
+    k_pos: torch.Tensor    # [B, keys]: 0..keys-1
+
+    @property
+    def flop(self) -> int:
+        B, S, H, D = self.q.shape
+        keys = self.k.shape[1]
+        return 4 * D * H * B * sum(keys - S + 1 + i for i in range(S))
+
+
+def prefill_chunk(device="cpu", seed: int = 0, B: int = 1, chunk: int = 128, keys: int = 32768,
+                  hq: int = 32, hkv: int = 8, d: int = 128, dtype=torch.bfloat16) -> PrefillChunk:
+    g = _gen(seed)
+    q = _randn(g, B, chunk, hq, d, dtype=dtype, device=device)
+    k = _randn(g, B, keys, hkv, d, dtype=dtype, device=device)
+    v = _randn(g, B, keys, hkv, d, dtype=dtype, device=device)
+    k_pos = torch.arange(keys).repeat(B, 1).to(device)
+    q_pos = torch.arange(keys - chunk, keys).repeat(B, 1).to(device)
+    return PrefillChunk(q, k, v, q_pos, k_pos)

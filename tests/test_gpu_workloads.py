@@ -1,4 +1,4 @@
-"""The five measured workloads at full size on the GPU.
+"""The measured attention workloads at full size on the GPU.
 
 * f32 attention (S=512, 8 heads, D=64) and its 2-way key split merged: both against the
   oracle, normwise rel <= 1e-5;
@@ -10,7 +10,9 @@
 * distributed-KV decode (B=32, cache 32768, 4 partitions): all 32 sequences against the
   oracle, and against one attention call over the whole cache (same property);
 * Ulysses share (65536 tokens, 8/2 heads, right padding): the full local attention against
-  the oracle on 1024 query rows spread over the valid tokens and 64 padded rows;
+  the oracle on all 26,644 valid query rows, the padded rows exactly (0, -inf);
+* prefill chunk (128 tokens against 32768 keys, 32/8 heads, the key-split route): every row
+  against the oracle;
 * linearity in V of the attention output at a production shape.
 bf16 tolerances are the ones of tests/_cases.py.
 """
@@ -147,6 +149,19 @@ def test_ulysses_share_full_size(cea, dev):
     assert (plain[:, :L].float().cpu() - ro).abs().max().item() <= 2e-2
     assert bool((out[:, L:] == 0).all()) and bool((lse[:, :, L:] == float("-inf")).all())
     assert bool((plain[:, L:] == 0).all())
+
+
+def test_prefill_chunk_full_size(cea, dev):
+    """The measured prefill chunk (key splits and two query heads per workgroup) against the
+    oracle on all 128 x 32 query rows, through attention_with_lse and plain attention."""
+    w = cea.workloads.prefill_chunk(device="cpu")
+    t = [x.to(dev) for x in (w.q, w.k, w.v, w.q_pos, w.k_pos)]
+    out, lse = cea.attention_with_lse(*t)
+    plain = cea.attention_fn(*t)
+    torch.cuda.synchronize()
+    ro, rl = ref.attention_with_lse(w.q, w.k, w.v, w.q_pos, w.k_pos)
+    assert_attention_close(out, lse, ro, rl, torch.bfloat16, "prefill chunk")
+    assert (plain.float().cpu() - ro).abs().max().item() <= 2e-2
 
 
 def test_output_is_linear_in_v(cea, dev):
