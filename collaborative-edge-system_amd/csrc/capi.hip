@@ -180,6 +180,16 @@ static DecodeUnits decode_units(int64_t Hq, int64_t Hkv, int64_t Sq, const HeadM
   return {(int32_t)Hq, 1, 1};
 }
 
+// A plan the decode launches can take: at most kDecodeMaxChunks chunks per batch row, batch
+// rows within the visibility pass's second grid dimension, and every grid within 31 bits
+// (the split kernel's: one work item per unit and chunk at most, before chunk pairs halve
+// it; the reduction's: one workgroup per output row).
+static bool decode_plan_fits(int64_t B, int64_t Sq, int64_t Hq, int64_t units,
+                             int64_t total_chunks) {
+  return total_chunks <= kDecodeMaxChunks && B < 65536 && B * units * total_chunks < INT32_MAX &&
+         B * Sq * Hq < INT32_MAX;
+}
+
 static DecodePlan plan_decode(const int64_t* Sk, int n, int64_t B, int64_t Sq, int64_t units,
                               int64_t G, int64_t D) {
   DecodePlan pl;
@@ -276,7 +286,9 @@ static bool use_decode(const AttnParams& p) {
   if (!decode_supported(p.Sq, p.Hq, p.Hkv, p.D, p.in_dtype, p.map)) return false;
   const int64_t sk = p.Sk;
   const DecodeUnits du = decode_units(p.Hq, p.Hkv, p.Sq, p.map);
-  if (plan_decode(&sk, 1, p.B, p.Sq, du.units, du.G, p.D).total_chunks > kDecodeMaxChunks) return false;
+  if (!decode_plan_fits(p.B, p.Sq, p.Hq, du.units,
+                        plan_decode(&sk, 1, p.B, p.Sq, du.units, du.G, p.D).total_chunks))
+    return false;
   if (!(p.out_dtype == CEA_F32 || p.out_dtype == p.in_dtype)) return false;
   if (p.accumulate && p.out_dtype != CEA_F32) return false;
   if (!(fabs(p.scale) >= 1e-30 && fabs(p.scale) <= 1e30)) return false;
@@ -970,7 +982,8 @@ int cea_partitioned_attention(const cea_tensor* q, int32_t n, const cea_tensor* 
     }
     if (dec) {
       const DecodeUnits du = decode_units(Hq, blocks[0].Hkv, Sq, blocks[0].map);
-      dec = plan_decode(sks, n, B, Sq, du.units, du.G, D).total_chunks <= kDecodeMaxChunks;
+      dec = decode_plan_fits(B, Sq, Hq, du.units,
+                             plan_decode(sks, n, B, Sq, du.units, du.G, D).total_chunks);
     }
     if (dec && part_out) {
       for (int i = 0; i < n && rc == 0; ++i) {
