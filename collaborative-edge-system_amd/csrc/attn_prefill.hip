@@ -7,7 +7,8 @@
 // optionally the exact online merge of merge_attention (attention.py:242-250) into a running
 // (out, lse) pair, as ring_attention does per step (sequence_parallel.py:117-121).
 //
-// Structure (one workgroup = 8 waves = 256 query rows of one query head, one per CU):
+// Structure (one workgroup = 8 waves = 256 query rows, one per CU; the rows of one query
+// head, or, for short query blocks, of 2, 4 or 8 query heads that read the same KV head):
 //   * every wave owns 32 query rows; its Q fragment stays in VGPRs for the whole kernel;
 //   * S^T = K.Q^T per 64-key tile with v_mfma_f32_32x32x16 (A = K from LDS, B = Q):
 //     lane (r, g) of the accumulator holds query row r and 16 of the 32 keys of a sub-tile,
@@ -27,7 +28,10 @@
 //   * the tiles a workgroup visits are listed up front from per-tile position summaries;
 //     each wave then computes a tile unmasked, element-masked or not at all from its own
 //     query-position range, so causal, zigzag and padding masks cost nothing on tiles that
-//     are entirely visible or entirely hidden.
+//     are entirely visible or entirely hidden;
+//   * a launch whose query blocks are too few to fill the device repeats its grid for up to
+//     16 key splits, each listing its own run of the block's tiles and writing a partial
+//     (out, lse) that the list merge combines.
 #include <string.h>
 
 #include <algorithm>
