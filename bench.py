@@ -556,7 +556,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # the shader clock settles over the first ~25 ms of back-to-back shares (the first
+    # dispatches of a process run up to 30 % slow): 20 warm-up shares (~40 ms) reach it
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of: ring,decode,layers,kvappend,ulysses,chunk,wire,f32,proj")
