@@ -8,11 +8,14 @@
 // weights (all lanes of a wave execute them together, so the redundancy costs no issue
 // slots).  The arithmetic follows the reference's rounding order: each weighted partial
 // is rounded before it is added, in the order of the partial list.
+#include <type_traits>
+
 #include "cea_kernels.hpp"
 
 namespace cea {
 
-template <typename A, typename O, int VEC>
+// NMAX >= p.n: the partials a launch can hold (registers for all of them are held at once)
+template <typename A, typename O, int VEC, int NMAX>
 __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   const int64_t nvec = p.D / VEC;
   const int64_t total = (int64_t)p.B * p.Sq * p.H * nvec;
@@ -25,17 +28,34 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   const int s = (int)(row % p.Sq);
   const int b = (int)(row / p.Sq);
 
-  // lse = logsumexp over the partials (n == 2 uses logaddexp, as merge_attention does)
-  A l[CEA_MAX_PARTS];
-  A m = neg_inf<A>();
+  // every partial's features and lse are loaded before any of the weights is computed: one
+  // memory round trip per thread, not one for the lses and another for the features
+  A x[NMAX][VEC];
+  A l[NMAX];
 #pragma unroll
-  for (int i = 0; i < CEA_MAX_PARTS; ++i) {
+  for (int i = 0; i < NMAX; ++i) {
     if (i < p.n) {
+      const A* op = (const A*)p.outs[i] + b * p.os[i][0] + s * p.os[i][1] + h * p.os[i][2] +
+                    (int64_t)dv * VEC;
+      if constexpr (VEC == 4 && sizeof(A) == 4) {
+        const float4 t = *(const float4*)op;
+        x[i][0] = t.x; x[i][1] = t.y; x[i][2] = t.z; x[i][3] = t.w;
+      } else if constexpr (VEC == 2 && sizeof(A) == 8) {
+        const double2 t = *(const double2*)op;
+        x[i][0] = t.x; x[i][1] = t.y;
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) x[i][e] = op[e];
+      }
       const A* lp = (const A*)p.lses[i];
       l[i] = lp[b * p.ls[i][0] + h * p.ls[i][1] + s * p.ls[i][2]];
-      m = l[i] > m ? l[i] : m;
     }
   }
+  // lse = logsumexp over the partials (n == 2 uses logaddexp, as merge_attention does)
+  A m = neg_inf<A>();
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i)
+    if (i < p.n) m = l[i] > m ? l[i] : m;
   A lse;
   if (p.pairwise) {
     lse = logaddexp<A>(l[0], l[1]);
@@ -43,7 +63,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
     const A shift = is_inf(m) ? (A)0 : m;  // logsumexp's infinite-max guard
     A sum = 0;
 #pragma unroll
-    for (int i = 0; i < CEA_MAX_PARTS; ++i)
+    for (int i = 0; i < NMAX; ++i)
       if (i < p.n) sum = add_rn(sum, exp_acc(l[i] - shift));
     lse = log_acc(sum) + shift;
   }
@@ -53,28 +73,15 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0;
 #pragma unroll
-  for (int i = 0; i < CEA_MAX_PARTS; ++i) {
+  for (int i = 0; i < NMAX; ++i) {
     if (i < p.n) {
       const A w = exp_acc(l[i] - safe);
-      const A* op = (const A*)p.outs[i] + b * p.os[i][0] + s * p.os[i][1] + h * p.os[i][2] +
-                    (int64_t)dv * VEC;
-      A x[VEC];
-      if constexpr (VEC == 4 && sizeof(A) == 4) {
-        float4 t = *(const float4*)op;
-        x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
-      } else if constexpr (VEC == 2 && sizeof(A) == 8) {
-        double2 t = *(const double2*)op;
-        x[0] = t.x; x[1] = t.y;
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) x[e] = op[e];
-      }
       if (i == 0) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] = mul_rn(x[e], w);
+        for (int e = 0; e < VEC; ++e) acc[e] = mul_rn(x[i][e], w);
       } else {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] = add_rn(acc[e], mul_rn(x[e], w));
+        for (int e = 0; e < VEC; ++e) acc[e] = add_rn(acc[e], mul_rn(x[i][e], w));
       }
     }
   }
@@ -121,19 +128,27 @@ int launch_merge(const MergeParams& p, hipStream_t st) {
   const int64_t blocks = (total + threads - 1) / threads;
   CEA_REQUIRE(blocks < (int64_t)1 << 31, CEA_EUNSUPPORTED, "merge: tensor too large");
   const dim3 grid((unsigned)blocks), block(threads);
-  if (p.dtype == CEA_F64) {
-    if (vec == 2) hipLaunchKernelGGL((merge_kernel<double, double, 2>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((merge_kernel<double, double, 1>), grid, block, 0, st, p);
-  } else if (p.out_dtype == CEA_BF16) {
-    if (vec == 4) hipLaunchKernelGGL((merge_kernel<float, bf16, 4>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((merge_kernel<float, bf16, 1>), grid, block, 0, st, p);
-  } else if (p.out_dtype == CEA_F16) {
-    if (vec == 4) hipLaunchKernelGGL((merge_kernel<float, f16, 4>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((merge_kernel<float, f16, 1>), grid, block, 0, st, p);
-  } else {
-    if (vec == 4) hipLaunchKernelGGL((merge_kernel<float, float, 4>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((merge_kernel<float, float, 1>), grid, block, 0, st, p);
-  }
+  auto go = [&](auto nmax) {
+    constexpr int NM = decltype(nmax)::value;
+    if (p.dtype == CEA_F64) {
+      if (vec == 2) hipLaunchKernelGGL((merge_kernel<double, double, 2, NM>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((merge_kernel<double, double, 1, NM>), grid, block, 0, st, p);
+    } else if (p.out_dtype == CEA_BF16) {
+      if (vec == 4) hipLaunchKernelGGL((merge_kernel<float, bf16, 4, NM>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((merge_kernel<float, bf16, 1, NM>), grid, block, 0, st, p);
+    } else if (p.out_dtype == CEA_F16) {
+      if (vec == 4) hipLaunchKernelGGL((merge_kernel<float, f16, 4, NM>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((merge_kernel<float, f16, 1, NM>), grid, block, 0, st, p);
+    } else {
+      if (vec == 4) hipLaunchKernelGGL((merge_kernel<float, float, 4, NM>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((merge_kernel<float, float, 1, NM>), grid, block, 0, st, p);
+    }
+  };
+  // registers for the partials a launch holds: few partials keep the kernel small (more
+  // waves in flight for the large two-way merges of ring steps)
+  if (p.n <= 2) go(std::integral_constant<int, 2>());
+  else if (p.n <= 4) go(std::integral_constant<int, 4>());
+  else go(std::integral_constant<int, CEA_MAX_PARTS>());
   CEA_CHECK_LAUNCH("merge");
   return CEA_OK;
 }
