@@ -6,7 +6,8 @@ of the matrix-core, f32 and generic kernels, every mask pattern of tests/_cases.
 and not, default / negative / small scales, kv_block splits, and partitioned (distributed-KV)
 calls with 1 to 5 partitions of random sizes through the split-KV decode route, and ring
 shares over 2 to 5 simulated ranks through the one-call route (empty and tiny blocks,
-padding, two batch rows, head sizes 64 and 128, regular and irregular maps).  The cases
+padding, two batch rows, head sizes 64 and 128, regular and irregular maps), and short query blocks against long key blocks
+(key splits, query heads packed per workgroup, decode units of part of a group).  The cases
 are drawn from a fixed seed, so a run is reproducible; tolerances are those of
 tests/_cases.py.
 """
@@ -83,6 +84,67 @@ def test_random_attention_matches_oracle(cea, dev, case):
         ro, rl = ref.attention_with_lse(q, k, v, qp, kp, causal=case.causal, scale=case.scale,
                                         kv_map=case.kv_map, kv_block=kv_block, route=route)
         assert_attention_close(out, lse, ro, rl, dtype, f"{case} {dtype}")
+
+
+def _long_key_cases(n=80, seed=9090):
+    """Short query blocks against long key blocks: the key-split prefill launches, query
+    heads packed 2-8 to a workgroup, and decode units of part of a KV head's group (up to 32
+    query heads per KV head)."""
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        D = rng.choice([64, 128])
+        Hkv = rng.choice([1, 2, 4])
+        G = rng.choice([1, 2, 4, 8, 16, 32])
+        Hq = Hkv * G
+        Sk = rng.choice([1500, 3000, 5000, 9000, 17000])
+        Sq = rng.choice([1, 2, 3, 5, 17, 40, 100, 130, 200])
+        while Sq * Sk * Hq > 60_000_000 and Sq > 1:  # keeps the oracle at about a second
+            Sq //= 2
+        kind = rng.choice(["decode", "random", "right_pad", "chunk", "chunk"])
+        causal = kind != "random" or rng.random() < 0.5
+        scale = rng.choice([None, None, -0.05, 0.3])
+        cases.append((rng.choice([1, 1, 2]), Sq, Sk, Hq, Hkv, D, kind, causal, scale, i))
+    return cases
+
+
+def _long_key_tensors(B, Sq, Sk, Hq, Hkv, D, kind, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Sq, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, Sk, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, Sk, Hkv, D, generator=g).to(dtype)
+    kp = torch.arange(Sk).repeat(B, 1)
+    end = torch.full((B,), Sk)
+    if kind == "right_pad":  # valid keys end early; rows past the end are padding too
+        end = torch.randint(Sq, Sk + 1, (B,), generator=g)
+        kp = torch.where(kp < end.view(-1, 1), kp, torch.full_like(kp, -1))
+    if kind == "random":
+        qp = torch.randint(0, Sk, (B, Sq), generator=g)
+    else:  # the last Sq valid positions (a chunk at the end, or decode tokens)
+        qp = end.view(-1, 1) - Sq + torch.arange(Sq).view(1, Sq)
+    return q, k, v, qp, kp
+
+
+LONG = _long_key_cases()
+
+
+@pytest.mark.parametrize("lc", LONG, ids=lambda c: "B{}-Sq{}-Sk{}-H{}/{}-D{}-{}-{}-s{}".format(
+    *c[:6], c[6], "c" if c[7] else "nc", c[8]))
+def test_random_short_queries_long_keys(cea, dev, lc):
+    B, Sq, Sk, Hq, Hkv, D, kind, causal, scale, seed = lc
+    dtype = torch.bfloat16 if seed % 2 == 0 else torch.float16
+    q, k, v, qp, kp = _long_key_tensors(B, Sq, Sk, Hq, Hkv, D, kind, seed, dtype)
+    print(f"long-key case {lc} {dtype}", flush=True)
+    out, lse = cea.attention_with_lse(q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev),
+                                      causal=causal, scale=scale)
+    plain = cea.attention.attention(q.to(dev), k.to(dev), v.to(dev), qp.to(dev), kp.to(dev),
+                                    causal=causal, scale=scale)
+    torch.cuda.synchronize()
+    route = "math" if scale is not None and scale <= 0 else "flash"
+    ro, rl = ref.attention_with_lse(q, k, v, qp, kp, causal=causal, scale=scale, route=route)
+    assert_attention_close(out, lse, ro, rl, dtype, str(lc))
+    assert plain.dtype == dtype
+    assert (plain.cpu().double() - ro.double()).abs().max().item() <= 2e-2, str(lc)
 
 
 def _partition_cases(n=48, seed=7177):
