@@ -299,9 +299,6 @@ static bool use_decode(const AttnParams& p) {
   return ((uintptr_t)p.q & 15) == 0 && ((uintptr_t)p.k & 15) == 0 && ((uintptr_t)p.v & 15) == 0;
 }
 
-// Runs one attention call with a prepared parameter block.  allow_decode = false keeps the
-// call off the split-KV decode kernels, whose workspace (chunk partials) is larger than the
-// tile summaries the other kernels need.
 // A prefill call whose query blocks alone give too few workgroups to fill the device (short
 // query blocks against long key blocks: prefill chunks, decode shapes the split-KV kernels do
 // not take): the block's tiles are dealt to S groups of workgroups, each writing a partial
@@ -344,6 +341,9 @@ static int run_prefill_split(const AttnParams& p, int S, char* ws, hipStream_t s
   return launch_merge(m, st);
 }
 
+// Runs one attention call with a prepared parameter block.  allow_decode = false keeps the
+// call off the split-KV decode kernels, whose workspace (chunk partials) is larger than the
+// tile summaries the other kernels need.
 static int run_attention(AttnParams& p, char* ws, size_t ws_bytes, hipStream_t st,
                          bool allow_decode = true) {
   if (allow_decode && p.Sk > 0 && use_decode(p))
