@@ -234,6 +234,47 @@ def test_workspace_counts_decode_partials_only_for_the_decode_route(cea):
     assert lib.cea_attention_workspace_bytes(B, 1, Hq, Sk, Hkv, 64, 1) > tiles
 
 
+def _split_plan(B, Sq, Hq, Sk, G):
+    """Key splits of a bf16 prefill launch, restated from the rule the library documents:
+    query heads per workgroup hp in {1, 2, 4, 8} (dividing G) with the fewest padded rows of
+    256 / hp per head, one on ties; splits only when the workgroups number fewer than 256,
+    then min(16, ceil(512 / workgroups), tiles // 8), at least 2."""
+    hp, best = 1, -(-Sq // 256) * 256 - Sq
+    for cand in (2, 4, 8):
+        if G % cand:
+            break
+        rows = 256 // cand
+        pad = -(-Sq // rows) * rows - Sq
+        if pad < best:
+            hp, best = cand, pad
+    grid = -(-Sq // (256 // hp)) * (Hq // hp) * B
+    if grid >= 256:
+        return 1
+    s = min(16, -(-512 // grid), -(-Sk // 64) // 8)
+    return s if s >= 2 else 1
+
+
+@pytest.mark.parametrize("B,Sq,Hq,Sk,Hkv,D", [
+    (1, 128, 32, 32768, 8, 128),   # a prefill chunk: two heads per workgroup, 16 splits
+    (1, 300, 8, 3000, 1, 64),      # G = 8
+    (4, 128, 32, 32768, 8, 128),   # 64 workgroups: 8 splits
+    (1, 8192, 32, 32768, 8, 128),  # the ring share's query block: no split
+    (1, 40, 8, 500, 2, 128),       # too few tiles to split
+    (2, 33, 6, 4000, 3, 64),       # G = 2
+])
+def test_workspace_holds_the_key_split_partials(cea, B, Sq, Hq, Sk, Hkv, D):
+    """For calls on the prefill route, cea_attention_workspace_bytes is the tile summaries
+    (32 bytes per 64-key tile and batch row, rounded up to 256) plus one f32 (out, lse) pair
+    per key split."""
+    lib = cea._native.load_library()
+    tiles = -(-B * -(-Sk // 64) * 32 // 256) * 256
+    S = _split_plan(B, Sq, Hq, Sk, Hq // Hkv)
+    partials = S * (B * Sq * Hq * D + B * Hq * Sq) * 4 if S > 1 else 0
+    assert lib.cea_attention_workspace_bytes(B, Sq, Hq, Sk, Hkv, D, 1) == tiles + partials
+    # f32 calls run other kernels: the summaries alone
+    assert lib.cea_attention_workspace_bytes(B, Sq, Hq, Sk, Hkv, D, 0) == tiles
+
+
 def _desc(nat, shape, dtype_code, addr):
     """A contiguous cea_tensor over a fake (aligned, never dereferenced) device address."""
     t = nat.CeaTensor()
