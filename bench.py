@@ -593,10 +593,10 @@ def main() -> int:
     only = set(filter(None, args.only.split(",")))
     want = lambda name: not only or name in only  # noqa: E731
 
-    w = sec = tflops = roof = None
-    if want("ring"):
-        _log("ring share (headline)")
-        w, sec, tflops, roof = bench_ring(cea, torch, args.steps, args.warmup, dev)
+    # The secondary lines run first and the headline right after them, with no idle gap: a
+    # GPU coming out of idle raises its shader clock over the first ~25 ms of back-to-back
+    # work (a process's first shares run up to 30 % slow), so W warm-up shares of a few
+    # milliseconds would leave part of the timed shares inside that ramp.
     secondary = {}
     if want("decode"):
         _log("distributed-KV decode")
@@ -624,6 +624,10 @@ def main() -> int:
     if want("proj"):
         _log("fused projections (gate/up + SiLU, Q/K/V)")
         secondary["projection"] = bench_projection(cea, torch, 10, max(5, args.warmup), dev)
+    w = sec = tflops = roof = None
+    if want("ring"):
+        _log("ring share (headline)")
+        w, sec, tflops, roof = bench_ring(cea, torch, args.steps, args.warmup, dev)
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline (oracle)")
