@@ -77,9 +77,20 @@ template <> __device__ __forceinline__ double widen<double, double>(double x) { 
 
 template <typename T, typename M> __device__ __forceinline__ T narrow(M x) { return (T)x; }
 
+// x rounded to bf16 (nearest even) and read back as f32 by one v_cvt_pk_bf16_f32 that puts
+// the rounded value in the high half and a zero in the low half: the word is then exactly
+// the f32 of that bf16, with no widening instruction (the compiler's own form of this
+// conversion adds a v_perm_b32)
+__device__ __forceinline__ float round_bf16(float x) {
+  uint32_t u;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(u) : "v"(x));
+  return __uint_as_float(u);
+}
+
 // value after a round trip through T (identity when T is the math type)
 template <typename T, typename M> __device__ __forceinline__ M rnd(M x) {
   if constexpr (sizeof(T) == sizeof(M)) return x;
+  else if constexpr (__is_same(T, bf16) && __is_same(M, float)) return round_bf16(x);
   else return widen<T, M>(narrow<T, M>(x));
 }
 
@@ -466,8 +477,15 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const M a = widen<T, M>(x1[r][e]), b = widen<T, M>(x2[r][e]);
-      acc += a * a;
-      acc += b * b;
+      if constexpr (__is_same(T, bf16) || __is_same(T, f16)) {
+        // the square of an f16 value, or of a bf16 value of magnitude at least 2^-63, is
+        // exact in f32, so one fma is the reference's h.pow(2) followed by the add
+        acc = __builtin_fmaf(a, a, acc);
+        acc = __builtin_fmaf(b, b, acc);
+      } else {
+        acc += a * a;
+        acc += b * b;
+      }
     }
     acc = wave_sum(acc);
     if ((threadIdx.x & 63) == 0) red[r][threadIdx.x >> 6] = acc;
@@ -475,7 +493,9 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
   __syncthreads();  // publishes the partial sums and the tables
   if (!active) return;
   if constexpr (__is_same(T, bf16)) {
-    // the same rounding points on pairs: every rounding of two values is one conversion
+    // the same rounding points, each one conversion that leaves the rounded value in f32;
+    // x and the weight stay packed between uses (widened where read), which keeps the kernel
+    // at 64 VGPRs: 8 waves per SIMD, the whole grid of a 4096-row call resident at once
     constexpr int NP = VEC / 2;
     uint32_t wp1[NP], wp2[NP];
     __builtin_memcpy(wp1, w1, 16);
@@ -496,21 +516,18 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_rows_kernel(
       }
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
-        // RMSNorm: yn = (x * rs).to(bf16); y = (w * yn).to(bf16)
-        const uint32_t yn1 = pack_bf16(mul_rn(bf16_lo(xp1[q]), rs), mul_rn(bf16_hi(xp1[q]), rs));
-        const uint32_t yn2 = pack_bf16(mul_rn(bf16_lo(xp2[q]), rs), mul_rn(bf16_hi(xp2[q]), rs));
-        const uint32_t y1 = pack_bf16(mul_rn(bf16_lo(wp1[q]), bf16_lo(yn1)), mul_rn(bf16_hi(wp1[q]), bf16_hi(yn1)));
-        const uint32_t y2 = pack_bf16(mul_rn(bf16_lo(wp2[q]), bf16_lo(yn2)), mul_rn(bf16_hi(wp2[q]), bf16_hi(yn2)));
-        const float a1[2] = {bf16_lo(y1), bf16_hi(y1)}, a2[2] = {bf16_lo(y2), bf16_hi(y2)};
+        const float xa1[2] = {bf16_lo(xp1[q]), bf16_hi(xp1[q])}, xa2[2] = {bf16_lo(xp2[q]), bf16_hi(xp2[q])};
+        const float wa1[2] = {bf16_lo(wp1[q]), bf16_hi(wp1[q])}, wa2[2] = {bf16_lo(wp2[q]), bf16_hi(wp2[q])};
         float r1[2], r2[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
+          // RMSNorm: yn = (x * rs).to(bf16); y = (w * yn).to(bf16)
+          const float y1 = round_bf16(mul_rn(wa1[u], round_bf16(mul_rn(xa1[u], rs))));
+          const float y2 = round_bf16(mul_rn(wa2[u], round_bf16(mul_rn(xa2[u], rs))));
           const float cv = cf[2 * q + u], sv = sf[2 * q + u];
           // first half: (y1*cos).to(bf16) + (-y2*sin).to(bf16); second: y2*cos + y1*sin
-          const uint32_t pq1 = pack_bf16(mul_rn(a1[u], cv), mul_rn(a2[u], sv));
-          const uint32_t pq2 = pack_bf16(mul_rn(a2[u], cv), mul_rn(a1[u], sv));
-          r1[u] = add_rn(bf16_lo(pq1), -bf16_hi(pq1));
-          r2[u] = add_rn(bf16_lo(pq2), bf16_hi(pq2));
+          r1[u] = add_rn(round_bf16(mul_rn(y1, cv)), -round_bf16(mul_rn(y2, sv)));
+          r2[u] = add_rn(round_bf16(mul_rn(y2, cv)), round_bf16(mul_rn(y1, sv)));
         }
         o1[q] = pack_bf16(r1[0], r1[1]);
         o2[q] = pack_bf16(r2[0], r2[1]);
