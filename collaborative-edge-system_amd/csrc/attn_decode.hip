@@ -114,6 +114,39 @@ __device__ __forceinline__ float sum_halves(float x) {
   const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
   return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
+// the same over the lane pairs l, l ^ 16 (v_permlane16_swap: rows 0 and 1, rows 2 and 3)
+__device__ __forceinline__ float max_rows16(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float sum_rows16(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+// max / sum over the 64 lanes, the result in every lane, without LDS round trips: each step
+// pairs every lane with one partner (xor 1 and xor 2 by DPP quad permutes, the quads of a
+// half-row by DPP row_half_mirror, the half-rows by row_mirror, then l ^ 16 and l ^ 32 by
+// the permlane swaps), so both lanes of a pair combine the same two values and all lanes
+// end with the bitwise same result
+#define CEA_DPP_F32(x, ctrl) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), (ctrl), 0xf, 0xf, false))
+__device__ __forceinline__ float wave_max_lanes(float v) {
+  v = __builtin_fmaxf(v, CEA_DPP_F32(v, 0xB1));   // quad_perm [1,0,3,2]
+  v = __builtin_fmaxf(v, CEA_DPP_F32(v, 0x4E));   // quad_perm [2,3,0,1]
+  v = __builtin_fmaxf(v, CEA_DPP_F32(v, 0x141));  // row_half_mirror
+  v = __builtin_fmaxf(v, CEA_DPP_F32(v, 0x140));  // row_mirror
+  return max_halves(max_rows16(v));
+}
+__device__ __forceinline__ float wave_sum_lanes(float v) {
+  v = v + CEA_DPP_F32(v, 0xB1);
+  v = v + CEA_DPP_F32(v, 0x4E);
+  v = v + CEA_DPP_F32(v, 0x141);
+  v = v + CEA_DPP_F32(v, 0x140);
+  return sum_halves(sum_rows16(v));
+}
+#undef CEA_DPP_F32
 
 __device__ __forceinline__ int part_of(const DecodeParams& p, int chunk) {
   int part = 0;
@@ -372,8 +405,7 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
       if (!vis) s[i] = -__builtin_inff();
     }
     float mx = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), __builtin_fmaxf(s[2], s[3]));
-    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = max_halves(mx);
+    mx = max_halves(max_rows16(mx));
     const bool grow = mx > m_run + grow_thr;
     if (__ballot(grow) != 0) {
       const float m_new = grow ? mx : m_run;
@@ -421,8 +453,7 @@ __global__ __launch_bounds__(DTHREADS, 2) void decode_split_kernel(const DecodeP
   }
 
   // ---- merge the waves of the workgroup and write the chunk partial
-  float l_row = l_run + __shfl_xor(l_run, 16, 64);
-  l_row = sum_halves(l_row);
+  const float l_row = sum_halves(sum_rows16(l_run));
   if (grp == 0 && row < NR) {
     red_m[wave][row] = m_run == -__builtin_inff() ? m_run : m_run * fabsf(scale);
     red_l[wave][row] = l_row;
@@ -545,14 +576,12 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
       const int c0 = ibegin[part], c1 = ibegin[part + 1];
       float mx = -__builtin_inff();
       for (int j = c0 + lane; j < c1; j += 64) mx = fmaxf(mx, m_s[j]);
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      mx = wave_max_lanes(mx);
       float l = 0.f;
       if (mx != -__builtin_inff())
         for (int j = c0 + lane; j < c1; j += 64)
           if (m_s[j] != -__builtin_inff()) l = __builtin_fmaf(w_s[j], expf(m_s[j] - mx), l);
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off, 64);
+      l = wave_sum_lanes(l);
       lp[part] = l > 0.f ? mx + logf(l) : -__builtin_inff();
     }
     float lse;
