@@ -558,49 +558,75 @@ __global__ __launch_bounds__(RTHREADS) void decode_reduce_kernel(const DecodePar
   }
   // items without a visible key wrote no partial: their weight is 0
   const uint64_t* cmask = p.tile_mask + (int64_t)b * total_chunks;
-  for (int j = tid; j < total; j += RTHREADS) {
+  auto item_ml = [&](int j) -> float2 {  // (m, l) of item j, (-inf, 0) for an empty item
     const DecodeItem it = item_of(p, b, j);
     const bool live = (cmask[it.chunk] | (it.nch > 1 ? cmask[it.chunk + 1] : 0ull)) != 0;
-    const float mv = base[j * cstride + D], lv = base[j * cstride + D + 1];
-    m_s[j] = live ? mv : -__builtin_inff();
-    w_s[j] = live ? lv : 0.f;  // l, replaced by the weight below
-  }
-  __syncthreads();
-  // statistics in wave 0 alone (wave shuffles, no workgroup barriers): per partition
-  // M_p = max m, L_p = sum l * exp(m - M_p), lse_p = M_p + log L_p; lse = logsumexp over the
-  // partitions (the reference merge's formula); chunk weights exp(m - lse)
+    const float2 ml = *(const float2*)(base + j * cstride + D);
+    return live ? ml : make_float2(-__builtin_inff(), 0.f);
+  };
+  // lse = logsumexp over the partitions' lse_p (the reference merge's formula)
+  auto combine = [&](const float (&lp)[CEA_MAX_PARTS]) -> float {
+    if (p.nparts == 1) return lp[0];
+    float mx = -__builtin_inff();
+    for (int part = 0; part < p.nparts; ++part) mx = fmaxf(mx, lp[part]);
+    const float shift = is_inf(mx) ? 0.f : mx;
+    float sum = 0.f;
+    for (int part = 0; part < p.nparts; ++part) sum = add_rn(sum, expf(lp[part] - shift));
+    return logf(sum) + shift;
+  };
+  // statistics in wave 0 alone (lane reductions, no workgroup barriers): per partition
+  // M_p = max m, L_p = sum l * exp(m - M_p), lse_p = M_p + log L_p; then lse and the item
+  // weights exp(m - lse)
   __shared__ float s_lse[CEA_MAX_PARTS + 1];
-  if (wave == 0) {
-    float lp[CEA_MAX_PARTS];
-    for (int part = 0; part < p.nparts; ++part) {
-      const int c0 = ibegin[part], c1 = ibegin[part + 1];
-      float mx = -__builtin_inff();
-      for (int j = c0 + lane; j < c1; j += 64) mx = fmaxf(mx, m_s[j]);
-      mx = wave_max_lanes(mx);
-      float l = 0.f;
-      if (mx != -__builtin_inff())
-        for (int j = c0 + lane; j < c1; j += 64)
-          if (m_s[j] != -__builtin_inff()) l = __builtin_fmaf(w_s[j], expf(m_s[j] - mx), l);
-      l = wave_sum_lanes(l);
-      lp[part] = l > 0.f ? mx + logf(l) : -__builtin_inff();
+  float lp[CEA_MAX_PARTS];
+  if (total <= 64) {
+    // one item per lane: its (m, l) stays in registers from the load to the weight, and the
+    // workgroup waits at one barrier (the weights) instead of two
+    if (wave == 0) {
+      const float2 ml = lane < total ? item_ml(lane) : make_float2(-__builtin_inff(), 0.f);
+      for (int part = 0; part < p.nparts; ++part) {
+        const bool in = lane >= ibegin[part] && lane < ibegin[part + 1];
+        const float mx = wave_max_lanes(in ? ml.x : -__builtin_inff());
+        const bool use = in && mx != -__builtin_inff() && ml.x != -__builtin_inff();
+        const float l = wave_sum_lanes(use ? ml.y * expf(ml.x - mx) : 0.f);
+        lp[part] = l > 0.f ? mx + logf(l) : -__builtin_inff();
+      }
+      const float lse = combine(lp);
+      const bool empty = lse == -__builtin_inff();
+      if (lane < total) w_s[lane] = (empty || ml.x == -__builtin_inff()) ? 0.f : expf(ml.x - lse);
+      if (lane == 0) {
+        for (int part = 0; part < p.nparts; ++part) s_lse[part] = lp[part];
+        s_lse[p.nparts] = lse;
+      }
     }
-    float lse;
-    if (p.nparts == 1) {
-      lse = lp[0];
-    } else {
-      float mx = -__builtin_inff();
-      for (int part = 0; part < p.nparts; ++part) mx = fmaxf(mx, lp[part]);
-      const float shift = is_inf(mx) ? 0.f : mx;
-      float sum = 0.f;
-      for (int part = 0; part < p.nparts; ++part) sum = add_rn(sum, expf(lp[part] - shift));
-      lse = logf(sum) + shift;
+  } else {
+    for (int j = tid; j < total; j += RTHREADS) {
+      const float2 ml = item_ml(j);
+      m_s[j] = ml.x;
+      w_s[j] = ml.y;  // l, replaced by the weight below
     }
-    const bool empty = lse == -__builtin_inff();
-    for (int j = lane; j < total; j += 64)
-      w_s[j] = (empty || m_s[j] == -__builtin_inff()) ? 0.f : expf(m_s[j] - lse);
-    if (lane == 0) {
-      for (int part = 0; part < p.nparts; ++part) s_lse[part] = lp[part];
-      s_lse[p.nparts] = lse;
+    __syncthreads();
+    if (wave == 0) {
+      for (int part = 0; part < p.nparts; ++part) {
+        const int c0 = ibegin[part], c1 = ibegin[part + 1];
+        float mx = -__builtin_inff();
+        for (int j = c0 + lane; j < c1; j += 64) mx = fmaxf(mx, m_s[j]);
+        mx = wave_max_lanes(mx);
+        float l = 0.f;
+        if (mx != -__builtin_inff())
+          for (int j = c0 + lane; j < c1; j += 64)
+            if (m_s[j] != -__builtin_inff()) l = __builtin_fmaf(w_s[j], expf(m_s[j] - mx), l);
+        l = wave_sum_lanes(l);
+        lp[part] = l > 0.f ? mx + logf(l) : -__builtin_inff();
+      }
+      const float lse = combine(lp);
+      const bool empty = lse == -__builtin_inff();
+      for (int j = lane; j < total; j += 64)
+        w_s[j] = (empty || m_s[j] == -__builtin_inff()) ? 0.f : expf(m_s[j] - lse);
+      if (lane == 0) {
+        for (int part = 0; part < p.nparts; ++part) s_lse[part] = lp[part];
+        s_lse[p.nparts] = lse;
+      }
     }
   }
   __syncthreads();
