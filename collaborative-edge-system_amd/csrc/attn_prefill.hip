@@ -202,13 +202,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void attn_prefill_kernel(const AttnPar
   const float grow_thr = kRescaleLog2 / c;  // raw-score growth that triggers a rescale
   const uint32_t qflip = scale < 0.f ? 0x80008000u : 0u;
 
+  // Under the causal rule a row with position < 0 (padding) sees no key and its scores are
+  // always masked, so its query features are not read (a workgroup of padding rows only
+  // writes its empty result).
   frag qf[D / 16];
   {
     const T* qrow = (const T*)p.q + b * p.qs_b + (int64_t)row * p.qs_s + h * p.qs_h;
+    const bool load_q = row_ok && !(p.causal && qpos < 0);
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
       uint4 raw = make_uint4(0, 0, 0, 0);
-      if (row_ok) raw = *(const uint4*)(qrow + ks * 16 + g * 8);
+      if (load_q) raw = *(const uint4*)(qrow + ks * 16 + g * 8);
       raw.x ^= qflip; raw.y ^= qflip; raw.z ^= qflip; raw.w ^= qflip;
       __builtin_memcpy(&qf[ks], &raw, 16);
     }
