@@ -202,6 +202,20 @@ __device__ __forceinline__ float exp_act(float x) {
   return __builtin_fmaf(p, lo * 0.693147180559945309417f, p);
 }
 
+// tanh(u) for the tanh form of GELU, whose value only enters as 1 + tanh(u): 1 - 2 / (e^(2u)
+// + 1), with e^(2u) from exp_act (within 2 ulp; 2u is exact) and the quotient from the
+// reciprocal with one FMA correction.  Its absolute error stays within a few units of 2^-24,
+// which the sum with 1 rounds away.  |u| is clamped to 10 first (tanh(10) and tanh(-10) round
+// to +-1 in f32, and e^(2u) stays finite); NaN passes the clamp and gives NaN.
+__device__ __forceinline__ float tanh_gelu_f32(float u) {
+  const float uc = u > 10.0f ? 10.0f : (u < -10.0f ? -10.0f : u);
+  const float d = exp_act(2.0f * uc) + 1.0f;
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q = 2.0f * r;
+  const float q2 = __builtin_fmaf(__builtin_fmaf(-d, q, 2.0f), r, q);  // q + (2 - d q) / d
+  return 1.0f - q2;
+}
+
 // silu(g) = g / (1 + e^-g) in f32: the quotient from the reciprocal with one FMA correction
 // (the correctly rounded quotient but in rare cases), and g / inf = -0 as in IEEE division.
 __device__ __forceinline__ float silu_f32(float g) {
@@ -225,7 +239,10 @@ template <int ACT, typename M> __device__ __forceinline__ M gate_act(M a) {
     const M kappa = (M)0.044715;
     const M cube = mul_rn(mul_rn(a, a), a);
     const M inner = mul_rn(beta, add_rn(a, mul_rn(kappa, cube)));
-    return mul_rn(mul_rn((M)0.5, a), add_rn((M)1, tanh_acc<M>(inner)));
+    if constexpr (sizeof(M) == 4)
+      return mul_rn(mul_rn((M)0.5, a), add_rn((M)1, tanh_gelu_f32(inner)));
+    else
+      return mul_rn(mul_rn((M)0.5, a), add_rn((M)1, tanh_acc<M>(inner)));
   } else {
     return a <= (M)0 ? (M)0 : a;
   }
