@@ -69,13 +69,22 @@ __device__ __forceinline__ void load_tile(F32Tile<D>& t, const float* kb, const 
   }
 }
 
+// max / sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the 16-lane rows of one query column)
+// by the gfx950 permlane swaps (no LDS round trip): each step combines the same two values
+// in both lanes of a pair, so every lane holds the bitwise same result
 __device__ __forceinline__ float xor_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
+  uint32_t u = __float_as_uint(x);
+  auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  u = __float_as_uint(fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+  sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
 }
 __device__ __forceinline__ float xor_sum(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
+  uint32_t u = __float_as_uint(x);
+  auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  u = __float_as_uint(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+  sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
 template <int D>
