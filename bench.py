@@ -593,23 +593,24 @@ def main() -> int:
     only = set(filter(None, args.only.split(",")))
     want = lambda name: not only or name in only  # noqa: E731
 
-    # The secondary lines run first and the headline right after them, with no idle gap: a
-    # GPU coming out of idle raises its shader clock over the first ~25 ms of back-to-back
-    # work (a process's first shares run up to 30 % slow), so W warm-up shares of a few
-    # milliseconds would leave part of the timed shares inside that ramp.
+    # The secondary lines run first (the graph-timed layer ops ahead of the decode, so no
+    # event-timed line is a process's first GPU work) and the headline right after them,
+    # with no idle gap: a GPU coming out of idle raises its shader clock over the first ~25 ms
+    # of back-to-back work (a process's first shares run up to 30 % slow), so W warm-up
+    # shares of a few milliseconds would leave part of the timed shares inside that ramp.
     secondary = {}
-    if want("decode"):
-        _log("distributed-KV decode")
-        secondary["kv_decode"] = bench_decode(cea, torch, args.steps, args.warmup, dev)
-        # the same step at the tinyllama-1.1b preset's heads (32 query / 4 KV, head size 64)
-        secondary["kv_decode_d64"] = bench_decode(cea, torch, args.steps, args.warmup, dev,
-                                                  hq=32, hkv=4, d=64)
     if want("layers"):
         _log("layer ops")
         secondary["layer_ops"] = bench_layers(cea, torch, args.steps, args.warmup, dev)
     if want("kvappend"):
         _log("kv-cache append")
         secondary["kv_append"] = bench_kv_append(cea, torch, args.steps, args.warmup, dev)
+    if want("decode"):
+        _log("distributed-KV decode")
+        secondary["kv_decode"] = bench_decode(cea, torch, args.steps, args.warmup, dev)
+        # the same step at the tinyllama-1.1b preset's heads (32 query / 4 KV, head size 64)
+        secondary["kv_decode_d64"] = bench_decode(cea, torch, args.steps, args.warmup, dev,
+                                                  hq=32, hkv=4, d=64)
     if want("ulysses"):
         _log("ulysses share")
         secondary["ulysses_share"] = bench_ulysses(cea, torch, max(5, args.steps // 2), args.warmup, dev)
